@@ -1,0 +1,207 @@
+// Standalone C++ bench of launch_scaled_mm (no torch), linking libfeatherops_amd.so.
+//
+// Same command line and report as the reference's
+// cpp_benchmarks/benchmark_scaled_mm_hip.cpp: --m --n --k --warmup --iters
+// --warps_m --warps_n --unroll --repeat_m --repeat_n; prints avg/std/min/max
+// ms, TFLOP/s and GB/s with GB = 2*M*K + N*K + 2*M*N bytes. Inputs follow the
+// same recipe (A uniform in [-1, 1) from mt19937(42); B drawn from the nine
+// e5m2 codes {0, +-0.25, +-0.5, +-0.75, +-1}; scale 2.34; bias uniform).
+// Additions: --out fp16|bf16, --rotate R (cycle through R distinct weight
+// buffers so that a weight larger than the 256 MB Infinity Cache in total is
+// streamed from HBM), --b e5m2|e4m3. Default config is the gfx950 256x256
+// tile (2,4,4,8,4).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <iomanip>
+#include <iostream>
+#include <numeric>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "featherops_amd.h"
+
+#define HIP_OK(expr)                                                                                     \
+    do {                                                                                                 \
+        const hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) {                                                                          \
+            std::cerr << "HIP error " << hipGetErrorString(e_) << " at " << __FILE__ << ":" << __LINE__ \
+                      << std::endl;                                                                      \
+            std::exit(1);                                                                                \
+        }                                                                                                \
+    } while (0)
+
+namespace {
+
+struct Opts {
+    int64_t m = 8192, n = 8192, k = 8192;
+    int warmup = 10, iters = 100;
+    int wm = 2, wn = 4, u = 4, rm = 8, rn = 4;
+    int out_bf16 = 0;
+    int b_dtype = FEATHER_B_E5M2;
+    int rotate = 1;
+};
+
+void usage(const char* argv0) {
+    std::cout << "Usage: " << argv0
+              << " [--m M] [--n N] [--k K] [--warmup W] [--iters I] [--warps_m M] [--warps_n N] [--unroll U]"
+                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R]\n";
+}
+
+Opts parse(int argc, char** argv) {
+    Opts o;
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        auto val = [&]() -> std::string {
+            if (i + 1 >= argc) {
+                std::cerr << "Missing value for " << a << std::endl;
+                std::exit(1);
+            }
+            return argv[++i];
+        };
+        if (a == "--m") o.m = std::stoll(val());
+        else if (a == "--n") o.n = std::stoll(val());
+        else if (a == "--k") o.k = std::stoll(val());
+        else if (a == "--warmup") o.warmup = std::stoi(val());
+        else if (a == "--iters") o.iters = std::stoi(val());
+        else if (a == "--warps_m") o.wm = std::stoi(val());
+        else if (a == "--warps_n") o.wn = std::stoi(val());
+        else if (a == "--unroll") o.u = std::stoi(val());
+        else if (a == "--repeat_m") o.rm = std::stoi(val());
+        else if (a == "--repeat_n") o.rn = std::stoi(val());
+        else if (a == "--out") o.out_bf16 = val() == "bf16";
+        else if (a == "--b") o.b_dtype = val() == "e4m3" ? FEATHER_B_E4M3FN : FEATHER_B_E5M2;
+        else if (a == "--rotate") o.rotate = std::max(1, std::stoi(val()));
+        else if (a == "--help" || a == "-h") {
+            usage(argv[0]);
+            std::exit(0);
+        } else {
+            std::cerr << "Unknown argument: " << a << std::endl;
+            usage(argv[0]);
+            std::exit(1);
+        }
+    }
+    if (o.m <= 0 || o.n <= 0 || o.k <= 0 || o.warmup < 0 || o.iters <= 0) {
+        std::cerr << "sizes and iters must be positive, warmup non-negative" << std::endl;
+        std::exit(1);
+    }
+    return o;
+}
+
+uint16_t to_half_bits(float f) {
+    const _Float16 h = static_cast<_Float16>(f);
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const Opts o = parse(argc, argv);
+    if (o.k % (16 * o.u) != 0) {
+        std::cerr << "K must be divisible by 16 * unroll_k (" << 16 * o.u << ")" << std::endl;
+        return 1;
+    }
+    const size_t na = static_cast<size_t>(o.m) * o.k, nb = static_cast<size_t>(o.k) * o.n,
+                 nc = static_cast<size_t>(o.m) * o.n;
+    const double bytes = 2.0 * na + 1.0 * nb + 2.0 * nc;
+    const double flops = 2.0 * o.m * o.n * o.k;
+
+    std::mt19937 gen(42);
+    std::uniform_real_distribution<float> uni(-1.f, 1.f);
+    std::vector<uint16_t> ha(na), hbias(o.n);
+    for (auto& x : ha) x = to_half_bits(uni(gen));
+    for (auto& x : hbias) x = to_half_bits(uni(gen));
+    static const uint8_t kCodes[] = {0xbc, 0xba, 0xb8, 0xb4, 0x00, 0x34, 0x38, 0x3a, 0x3c};
+    std::uniform_int_distribution<int> pick(0, 8);
+    std::vector<uint8_t> hb(nb);
+    for (auto& x : hb) x = kCodes[pick(gen)];
+
+    void *da, *dbias, *dc;
+    float* dscale;
+    std::vector<uint8_t*> db(o.rotate);
+    HIP_OK(hipMalloc(&da, na * 2));
+    HIP_OK(hipMalloc(&dbias, o.n * 2));
+    HIP_OK(hipMalloc(&dc, nc * 2));
+    HIP_OK(hipMalloc(&dscale, sizeof(float)));
+    for (auto& p : db) {
+        HIP_OK(hipMalloc(&p, nb));
+        HIP_OK(hipMemcpy(p, hb.data(), nb, hipMemcpyHostToDevice));
+    }
+    HIP_OK(hipMemcpy(da, ha.data(), na * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dbias, hbias.data(), o.n * 2, hipMemcpyHostToDevice));
+    const float hs = 2.34f;
+    HIP_OK(hipMemcpy(dscale, &hs, sizeof(float), hipMemcpyHostToDevice));
+
+    hipStream_t stream;
+    hipEvent_t t0, t1;
+    HIP_OK(hipStreamCreate(&stream));
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+
+    auto run = [&](int i) {
+        const bool ok = launch_scaled_mm(da, db[i % o.rotate], dscale, static_cast<const uint16_t*>(dbias),
+                                         static_cast<uint16_t*>(dc), o.m, o.n, o.k, 1, 1, o.wm, o.wn, o.u, o.rm, o.rn,
+                                         o.b_dtype, o.out_bf16, stream);
+        if (!ok) {
+            std::cerr << "Failed to launch kernel: unsupported config" << std::endl;
+            std::exit(1);
+        }
+    };
+    for (int i = 0; i < o.warmup; ++i) run(i);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipStreamSynchronize(stream));
+
+    std::vector<float> ms(o.iters);
+    for (int i = 0; i < o.iters; ++i) {
+        HIP_OK(hipEventRecord(t0, stream));
+        run(i);
+        HIP_OK(hipEventRecord(t1, stream));
+        HIP_OK(hipEventSynchronize(t1));
+        HIP_OK(hipEventElapsedTime(&ms[i], t0, t1));
+    }
+    // back-to-back launches, one event pair: the steady-state rate without per-call event gaps
+    HIP_OK(hipEventRecord(t0, stream));
+    for (int i = 0; i < o.iters; ++i) run(i);
+    HIP_OK(hipEventRecord(t1, stream));
+    HIP_OK(hipEventSynchronize(t1));
+    float stream_ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&stream_ms, t0, t1));
+    stream_ms /= o.iters;
+
+    const double avg = std::accumulate(ms.begin(), ms.end(), 0.0) / ms.size();
+    double var = 0.0;
+    for (float x : ms) var += (x - avg) * (x - avg);
+    const double sd = std::sqrt(var / ms.size());
+    std::cout << std::fixed << std::setprecision(3);
+    std::cout << "scaled_mm benchmark\n";
+    std::cout << "  problem: m=" << o.m << " n=" << o.n << " k=" << o.k << (o.out_bf16 ? " out=bf16" : " out=fp16")
+              << " rotate=" << o.rotate << "\n";
+    std::cout << "  config: warps_m=" << o.wm << " warps_n=" << o.wn << " unroll_k=" << o.u << " repeat_m=" << o.rm
+              << " repeat_n=" << o.rn << " kernel_id="
+              << feather_scaled_mm_kernel_id(o.m, o.n, o.k, o.wm, o.wn, o.u, o.rm, o.rn) << "\n";
+    std::cout << "  memory footprint: " << bytes / (1024.0 * 1024.0) << " MiB\n";
+    std::cout << "  avg ms: " << avg << "\n  std ms: " << sd << "\n";
+    std::cout << "  min ms: " << *std::min_element(ms.begin(), ms.end()) << "\n";
+    std::cout << "  max ms: " << *std::max_element(ms.begin(), ms.end()) << "\n";
+    std::cout << "  avg TFLOP/s: " << flops / avg / 1e9 << "\n";
+    std::cout << "  avg GB/s: " << bytes / avg / 1e6 << "\n";
+    std::cout << "  back-to-back ms: " << stream_ms << "  (TFLOP/s " << flops / stream_ms / 1e9 << ", GB/s "
+              << bytes / stream_ms / 1e6 << ")" << std::endl;
+
+    HIP_OK(hipEventDestroy(t0));
+    HIP_OK(hipEventDestroy(t1));
+    HIP_OK(hipStreamDestroy(stream));
+    for (auto p : db) HIP_OK(hipFree(p));
+    HIP_OK(hipFree(da));
+    HIP_OK(hipFree(dbias));
+    HIP_OK(hipFree(dc));
+    HIP_OK(hipFree(dscale));
+    return 0;
+}

@@ -1,0 +1,200 @@
+// extern "C" entry points of libfeatherops_amd.so (declared in
+// include/featherops_amd.h). Validation that needs only sizes and pointers
+// lives here; dtype/stride checks of torch tensors live in the Python layer.
+#include <stdint.h>
+
+#include "featherops_amd.h"
+#include "quant_prepack.h"
+#include "scaled_mm_dispatch.h"
+
+namespace {
+
+using feather::KernelId;
+
+struct Cfg {
+    int wm, wn, u, rm, rn;
+};
+
+// Reference configurations (kernel/hip/hip_kernel.py:60-89, hip_kernel.cu:603-630)
+// followed by two gfx950 tiles the reference has no tuple for.
+constexpr Cfg kConfigs[] = {
+    {1, 1, 2, 1, 2}, {1, 1, 4, 1, 2}, {1, 2, 2, 1, 2}, {1, 2, 4, 1, 2}, {1, 4, 2, 1, 2}, {1, 4, 4, 1, 2},
+    {1, 8, 2, 1, 2}, {1, 8, 4, 1, 2}, {1, 1, 2, 2, 2}, {1, 1, 4, 2, 2}, {1, 1, 2, 4, 4}, {1, 1, 4, 4, 4},
+    {1, 2, 2, 2, 2}, {1, 2, 4, 2, 2}, {2, 1, 2, 2, 2}, {2, 1, 4, 2, 2}, {1, 4, 2, 4, 2}, {1, 4, 4, 4, 2},
+    {1, 8, 2, 8, 2}, {1, 8, 4, 8, 2}, {2, 2, 2, 4, 4}, {2, 2, 4, 4, 4}, {2, 4, 2, 4, 2}, {2, 4, 4, 4, 2},
+    {2, 4, 2, 4, 4}, {2, 4, 4, 4, 4}, {4, 2, 2, 2, 4}, {4, 2, 4, 2, 4},
+    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4},
+};
+
+bool known_config(int wm, int wn, int u, int rm, int rn) {
+    for (const Cfg& c : kConfigs)
+        if (c.wm == wm && c.wn == wn && c.u == u && c.rm == rm && c.rn == rn) return true;
+    return false;
+}
+
+int kernel_for(int64_t M, int wm, int wn, int rm, int rn) {
+    if (M <= 64) return feather::kSmallM;
+    const int bm = 16 * wm * rm;
+    const int bn = 16 * wn * rn;
+    if (bm >= 256 && bn >= 256) return feather::kTile256x256;
+    if (bm >= 256) return feather::kTile256x128;
+    if (bn >= 256) return bm >= 128 ? feather::kTile128x256 : feather::kTile64x128;
+    if (bm >= 128 && bn >= 128) return feather::kTile128x128;
+    if (bn >= 128) return feather::kTile64x128;
+    return feather::kTile64x64;
+}
+
+bool sizes_ok(int64_t M, int64_t N, int64_t K) {
+    const int64_t lim = INT32_MAX;
+    return M >= 0 && N > 0 && K > 0 && M <= lim && N <= lim && K <= lim && N % 16 == 0 && K % 16 == 0 &&
+           (K / 16) * N <= lim;
+}
+
+int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n, int unroll_k,
+                                int repeat_m, int repeat_n) {
+    if (!known_config(block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n)) return feather::kKernelNone;
+    if (!sizes_ok(M, N, K)) return feather::kKernelNone;
+    return kernel_for(M, block_warps_m, block_warps_n, repeat_m, repeat_n);
+}
+
+bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,
+                      int64_t M, int64_t N, int64_t K, int has_scale, int has_bias, int block_warps_m,
+                      int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype, int output_dtype,
+                      hipStream_t stream) {
+    const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    if (kid == feather::kKernelNone) return false;
+    if (b_dtype != FEATHER_B_E4M3FN && b_dtype != FEATHER_B_E5M2) return false;
+    if (output_dtype != 0 && output_dtype != 1) return false;
+    if (M == 0) return true;
+    feather::MmArgs p;
+    p.a = static_cast<const uint16_t*>(a);
+    p.b = b_prepacked;
+    p.scale = scale;
+    p.bias = bias;
+    p.c = c;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.has_scale = has_scale ? 1 : 0;
+    p.has_bias = has_bias ? 1 : 0;
+    p.out_bf16 = output_dtype == 1;
+    p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
+    p.group_m = 0;
+    if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, stream);
+    return feather::launch_tile_kernel(kid, p, stream);
+}
+
+int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,
+                                  int native, uint8_t* out, float* scale_out, uint32_t* workspace, hipStream_t stream) {
+    if (!w || !out || !scale_out || !workspace) return FEATHER_ERR_INVALID;
+    if (w_dtype != FEATHER_DTYPE_F16 && w_dtype != FEATHER_DTYPE_BF16 && w_dtype != FEATHER_DTYPE_F32)
+        return FEATHER_ERR_INVALID;
+    if (N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX || (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
+    feather::QuantArgs q;
+    q.w = w;
+    q.dtype = w_dtype;
+    q.N = N;
+    q.K = K;
+    q.ckpt_scale = ckpt_scale;
+    q.native = native != 0;
+    q.out = out;
+    q.scale_out = scale_out;
+    q.workspace = workspace;
+    q.scale_in = nullptr;
+    feather::launch_quantize_prepack(q, stream);
+    return launch_status();
+}
+
+int feather_quantize_prepack_e5m2_scaled(const void* w, int w_dtype, int64_t N, int64_t K, const float* scale,
+                                         uint8_t* out, hipStream_t stream) {
+    if (!w || !out || !scale) return FEATHER_ERR_INVALID;
+    if (w_dtype != FEATHER_DTYPE_F16 && w_dtype != FEATHER_DTYPE_BF16 && w_dtype != FEATHER_DTYPE_F32)
+        return FEATHER_ERR_INVALID;
+    if (N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX || (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
+    feather::QuantArgs q;
+    q.w = w;
+    q.dtype = w_dtype;
+    q.N = N;
+    q.K = K;
+    q.ckpt_scale = nullptr;
+    q.native = true;
+    q.out = out;
+    q.scale_out = nullptr;
+    q.workspace = nullptr;
+    q.scale_in = scale;
+    feather::launch_quantize_prepack(q, stream);
+    return launch_status();
+}
+
+int feather_prepack_transpose(const uint8_t* w_nk, uint8_t* out, int64_t N, int64_t K, hipStream_t stream) {
+    if (!w_nk || !out || N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX || (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(w_nk) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u))
+        return FEATHER_ERR_INVALID;
+    feather::launch_chunk_transpose(w_nk, out, N, K, 0, stream);
+    return launch_status();
+}
+
+int feather_unprepack_transpose(const uint8_t* packed, uint8_t* out_nk, int64_t N, int64_t K, hipStream_t stream) {
+    if (!packed || !out_nk || N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX ||
+        (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(packed) & 15u) || (reinterpret_cast<uintptr_t>(out_nk) & 15u))
+        return FEATHER_ERR_INVALID;
+    feather::launch_chunk_transpose(packed, out_nk, N, K, 1, stream);
+    return launch_status();
+}
+
+int feather_prepack_b(const uint8_t* b_kn, uint8_t* out, int64_t K, int64_t N, hipStream_t stream) {
+    if (!b_kn || !out || N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K / 16 > 65535 ||
+        K * N > INT64_C(1) << 40)
+        return FEATHER_ERR_INVALID;
+    if (reinterpret_cast<uintptr_t>(out) & 15u) return FEATHER_ERR_INVALID;
+    feather::launch_prepack_kn(b_kn, out, K, N, stream);
+    return launch_status();
+}
+
+int feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream) {
+    if (n < 0 || (n > 0 && (!in || !out))) return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(in) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
+    if (n == 0) return FEATHER_OK;
+    feather::launch_bf16_to_fp16(in, out, n, stream);
+    return launch_status();
+}
+
+int feather_dequantize_e5m2(const uint8_t* packed, const float* scale, void* out, int out_dtype, int64_t N, int64_t K,
+                            hipStream_t stream) {
+    if (!packed || !scale || !out || N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX ||
+        (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if (out_dtype != FEATHER_DTYPE_F16 && out_dtype != FEATHER_DTYPE_BF16 && out_dtype != FEATHER_DTYPE_F32)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(packed) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u))
+        return FEATHER_ERR_INVALID;
+    feather::launch_dequant(packed, scale, out, N, K, out_dtype, stream);
+    return launch_status();
+}
+
+const char* feather_status_string(int status) {
+    switch (status) {
+        case FEATHER_OK: return "ok";
+        case FEATHER_ERR_INVALID: return "invalid argument";
+        case FEATHER_ERR_UNSUPPORTED: return "unsupported configuration";
+        case FEATHER_ERR_LAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+int feather_abi_version(void) { return 1; }
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// Shared device helpers for the gfx950 (CDNA4) FeatherOps kernels.
+//
+// Number formats handled here:
+//   fp8 e5m2   [s:1][e:5][m:2], bias 15 -- the same exponent field and bias as
+//              fp16, so widening a code to fp16 is the byte placed in the high
+//              half of the 16-bit word (exact for all 256 codes, including
+//              subnormals, +-inf and NaN).
+//   fp8 e4m3fn [s:1][e:4][m:3], bias 7, no inf, NaN = 0x7f/0xff.
+//   fp16 / bf16 outputs, rounded to nearest-even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace feather {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Workgroups of one dispatch are handed to the 8 XCDs of an MI355X
+// round-robin: workgroup p runs on XCD p % 8.
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return bits_f32(static_cast<uint32_t>(b) << 16); }
+
+// fp32 -> fp16, round to nearest even; overflow goes to +-inf (v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t f32_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// fp32 -> bf16, round to nearest even; NaN becomes the canonical 0x7fc0,
+// which is what torch's float -> bfloat16 conversion produces.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = f32_bits(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ uint16_t f32_to_out_bits(float f) {
+    if constexpr (kBf16) return f32_to_bf16_bits(f);
+    else return f32_to_half_bits(f);
+}
+template <bool kBf16>
+__device__ __forceinline__ float out_bits_to_f32(uint16_t b) {
+    if constexpr (kBf16) return bf16_bits_to_f32(b);
+    else return half_bits_to_f32(b);
+}
+
+// Widen 8 fp8 bytes (two dwords, byte j = element j) into 8 fp16 lanes.
+// e5m2: element j -> (byte_j << 8); one v_perm_b32 per output dword.
+// e4m3fn: element j -> ((byte_j & 0x7f) << 7) | ((byte_j & 0x80) << 8), i.e.
+// the code re-read with fp16's bias, which is the true value * 2^-8 for every
+// finite code (subnormals included); the caller multiplies the fp32 result by
+// 256. The two NaN codes decode to the finite +-1.875*2^-8.
+template <bool kE4m3>
+__device__ __forceinline__ half8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
+    uint32_t w0, w1, w2, w3;
+    if constexpr (!kE4m3) {
+        // selector bytes: 0x0c -> 0x00, 0..3 -> bytes of the second operand
+        w0 = __builtin_amdgcn_perm(0u, lo, 0x010c000cu);
+        w1 = __builtin_amdgcn_perm(0u, lo, 0x030c020cu);
+        w2 = __builtin_amdgcn_perm(0u, hi, 0x010c000cu);
+        w3 = __builtin_amdgcn_perm(0u, hi, 0x030c020cu);
+    } else {
+        const uint32_t p0 = __builtin_amdgcn_perm(0u, lo, 0x0c010c00u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0u, lo, 0x0c030c02u);
+        const uint32_t p2 = __builtin_amdgcn_perm(0u, hi, 0x0c010c00u);
+        const uint32_t p3 = __builtin_amdgcn_perm(0u, hi, 0x0c030c02u);
+        w0 = ((p0 & 0x007f007fu) << 7) | ((p0 & 0x00800080u) << 8);
+        w1 = ((p1 & 0x007f007fu) << 7) | ((p1 & 0x00800080u) << 8);
+        w2 = ((p2 & 0x007f007fu) << 7) | ((p2 & 0x00800080u) << 8);
+        w3 = ((p3 & 0x007f007fu) << 7) | ((p3 & 0x00800080u) << 8);
+    }
+    uint4 v = make_uint4(w0, w1, w2, w3);
+    return __builtin_bit_cast(half8_t, v);
+}
+
+// v holds 8 output values (16-bit each); adds bias[0..7] elementwise in the
+// output type: both operands to fp32 (exact), add, one rounding to the output
+// type. For fp16 this equals a native fp16 add (24 >= 2*11+2 bits).
+template <bool kBf16>
+__device__ __forceinline__ void add_bias8(uint4& v, const uint16_t* bias) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] & 0xffffu)) + out_bits_to_f32<kBf16>(bias[2 * i]);
+        const float hi = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] >> 16)) + out_bits_to_f32<kBf16>(bias[2 * i + 1]);
+        w[i] = static_cast<uint32_t>(f32_to_out_bits<kBf16>(lo)) | (static_cast<uint32_t>(f32_to_out_bits<kBf16>(hi)) << 16);
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+// D(16x16,f32) += A(16x32,f16) * B(32x16,f16). Lane l supplies A row l%16 and
+// B column l%16 with 8 consecutive K slots each; lanes l and l+16*g share the
+// row/column and cover slot groups g = 0..3. Any K order that is the same for
+// the A and the B operand gives the same sum, which the kernels rely on.
+__device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace feather

@@ -1,0 +1,31 @@
+// Host launchers for the quantize / layout / cast kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace feather {
+
+// element types of weights and dequantized outputs (values shared with the C ABI)
+enum WeightDtype : int { kDtypeF16 = 0, kDtypeBF16 = 1, kDtypeF32 = 2 };
+
+struct QuantArgs {
+    const void* w;            // (N, K) row-major, dtype
+    int dtype;
+    int64_t N, K;
+    const float* ckpt_scale;  // device scalar or null (load path only)
+    bool native;              // false: load path (fp32), true: patch path (weight dtype)
+    uint8_t* out;             // (K/16, N, 16) e5m2 bytes
+    float* scale_out;         // device scalar
+    uint32_t* workspace;      // >= 4 bytes of device memory (unused when scale_in is set)
+    const float* scale_in;    // device scalar: use this scale instead of recalculating (native only)
+};
+
+void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream);
+void launch_chunk_transpose(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int dir, hipStream_t stream);
+void launch_prepack_kn(const uint8_t* src, uint8_t* dst, int64_t K, int64_t N, hipStream_t stream);
+void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+void launch_dequant(const uint8_t* src, const float* scale, void* dst, int64_t N, int64_t K, int dtype,
+                    hipStream_t stream);
+
+}  // namespace feather

@@ -1,0 +1,380 @@
+// Weight quantize-and-prepack, layout transforms and the bf16 -> fp16 cast.
+//
+// Quantize follows comfy_feather/quant.py:52-74 (quantize_fp8e5m2_scaled) in
+// the two ways the reference calls it:
+//   load path  (quant.py:116-136, make_feather_quantized_weight):
+//       x = float32(w) * ckpt_scale; s = amax|x| / 57344; s==0 -> 1;
+//       q = e5m2(x * (1/s))                        -- all fp32
+//   patch path (quant.py:81-96,139-146, quantize_feather_weight):
+//       arithmetic in the weight's own dtype T: s = float32(amax|w|) / 57344;
+//       s==0 -> 1; for T = fp16 only, s = 1 / clamp(1/s, -65504, 65504);
+//       inv = T(1/s); q = e5m2(T(w * inv))
+// followed by the prepack of quant.py:11-13: (N, K) -> (K/16, N, 16).
+// Every division is the IEEE-correctly-rounded fp32 one (hipcc's default), as
+// torch's CPU division is, and the fp32 -> e5m2 conversion matches torch's
+// c10 conversion: round to nearest even, |x| >= 61440 -> +-inf, NaN -> 0x7f
+// with the sign bit kept.
+//
+// Two kernels: a grid-stride amax that folds per-workgroup maxima into one
+// 32-bit word with a vector atomicMax, then a streaming quantize that
+// recomputes the scale from that word in every thread and writes the
+// prepacked bytes directly (16 output bytes per thread, 1 KB contiguous per
+// wave).
+#include "feather_common.h"
+#include "quant_prepack.h"
+
+namespace feather {
+namespace {
+
+constexpr float kE5m2Max = 57344.0f;
+constexpr float kFp16Max = 65504.0f;
+
+// fp32 -> fp8 e5m2, round to nearest even, |x| >= 61440 -> inf.
+__device__ __forceinline__ uint32_t f32_to_e5m2(float f) {
+    const uint32_t u = f32_bits(f);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    uint32_t r;
+    if (a > 0x7f800000u) {
+        r = 0x7fu;                          // NaN
+    } else if (a >= 0x47700000u) {          // 61440.0f: ties to even go up to 2^16 = inf
+        r = 0x7cu;
+    } else if (a >= 0x38800000u) {          // >= 2^-14: normal e5m2
+        const uint32_t lsb = (a >> 21) & 1u;
+        r = ((a + 0x000fffffu + lsb) >> 21) - (112u << 2);  // re-bias exponent 127 -> 15
+    } else {                                // subnormal: multiples of 2^-16, exact scaling, RNE
+        r = static_cast<uint32_t>(__builtin_rintf(bits_f32(a) * 65536.0f));
+    }
+    return r | sign;
+}
+
+template <int DT>
+struct WeightType;
+template <>
+struct WeightType<kDtypeF16> {
+    __device__ static float load(const void* p, int64_t i) { return half_bits_to_f32(static_cast<const uint16_t*>(p)[i]); }
+    __device__ static float round(float f) { return half_bits_to_f32(f32_to_half_bits(f)); }
+};
+template <>
+struct WeightType<kDtypeBF16> {
+    __device__ static float load(const void* p, int64_t i) { return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]); }
+    __device__ static float round(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+};
+template <>
+struct WeightType<kDtypeF32> {
+    __device__ static float load(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+    __device__ static float round(float f) { return f; }
+};
+
+// 16 consecutive elements starting at element index i (16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load16(const void* p, int64_t i, float (&v)[16]) {
+    if constexpr (DT == kDtypeF32) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 t = q[j];
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        }
+    } else {
+        const uint4* q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint4 t = q[j];
+            const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint16_t lo = static_cast<uint16_t>(w[h] & 0xffffu), hi = static_cast<uint16_t>(w[h] >> 16);
+                if constexpr (DT == kDtypeF16) {
+                    v[8 * j + 2 * h] = half_bits_to_f32(lo); v[8 * j + 2 * h + 1] = half_bits_to_f32(hi);
+                } else {
+                    v[8 * j + 2 * h] = bf16_bits_to_f32(lo); v[8 * j + 2 * h + 1] = bf16_bits_to_f32(hi);
+                }
+            }
+        }
+    }
+}
+
+__global__ void zero_word_kernel(uint32_t* w) { w[0] = 0u; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// amax of |x| (load path: x = w * ckpt_scale) as fp32 bits; NaN bit patterns
+// compare above +inf, so a NaN anywhere yields a NaN amax as torch.amax does.
+template <int DT>
+__global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ w, int64_t n,
+                                                   const float* __restrict__ ckpt_scale, int premul,
+                                                   uint32_t* __restrict__ amax_bits) {
+    __shared__ uint32_t part[4];
+    const float cs = (premul && ckpt_scale) ? ckpt_scale[0] : 1.0f;
+    uint32_t m = 0u;
+    const int64_t ngroups = n / 16;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+        float v[16];
+        load16<DT>(w, g * 16, v);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t b = f32_bits(premul ? v[j] * cs : v[j]) & 0x7fffffffu;
+            m = b > m ? b : m;
+        }
+    }
+    // tail (n % 16 elements) handled by the first threads of block 0
+    if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
+        const float x = WeightType<DT>::load(w, ngroups * 16 + threadIdx.x);
+        const uint32_t b = f32_bits(premul ? x * cs : x) & 0x7fffffffu;
+        m = b > m ? b : m;
+    }
+    m = wave_max_u32(m);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t r = part[0];
+        for (int i = 1; i < 4; ++i) r = part[i] > r ? part[i] : r;
+        atomicMax(amax_bits, r);
+    }
+}
+
+// scale from amax, exactly as the reference's torch ops compute it
+template <int DT>
+__device__ __forceinline__ float scale_from_amax(uint32_t amax_bits, bool native) {
+    float s = bits_f32(amax_bits) / kE5m2Max;
+    if (s == 0.0f) s = 1.0f;
+    if (native && DT == kDtypeF16) {
+        float r = 1.0f / s;
+        r = r < -kFp16Max ? -kFp16Max : (r > kFp16Max ? kFp16Max : r);  // NaN passes through
+        s = 1.0f / r;
+    }
+    return s;
+}
+
+// grid: (ceil(K/16 / 4), ceil(N / 64)); block 256 = 64 rows (n) x 4 K-groups.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restrict__ w, int N, int K,
+                                                            const float* __restrict__ ckpt_scale, int native,
+                                                            const uint32_t* __restrict__ amax_bits,
+                                                            const float* __restrict__ scale_in,
+                                                            uint8_t* __restrict__ out, float* __restrict__ scale_out) {
+    // scale_in: caller-supplied scale (quant.py:59-62), no recalculation and no clamp
+    const float s = scale_in ? scale_in[0] : scale_from_amax<DT>(amax_bits[0], native != 0);
+    if (scale_out && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) scale_out[0] = s;
+    const int n = blockIdx.y * 64 + (threadIdx.x & 63);
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N || i >= (K >> 4)) return;
+
+    float v[16];
+    load16<DT>(w, static_cast<int64_t>(n) * K + i * 16, v);
+    uint32_t q[16];
+    if (native) {
+        const float inv = WeightType<DT>::round(1.0f / s);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2(WeightType<DT>::round(v[j] * inv));
+    } else {
+        const float cs = ckpt_scale ? ckpt_scale[0] : 1.0f;
+        const float inv = 1.0f / s;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2((v[j] * cs) * inv);
+    }
+    uint4 o;
+    o.x = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+    o.y = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+    o.z = q[8] | (q[9] << 8) | (q[10] << 16) | (q[11] << 24);
+    o.w = q[12] | (q[13] << 8) | (q[14] << 16) | (q[15] << 24);
+    *reinterpret_cast<uint4*>(out + (static_cast<int64_t>(i) * N + n) * 16) = o;
+}
+
+// (N, K) bytes -> (K/16, N, 16) (dir 0) or back (dir 1): moves 16-byte chunks.
+__global__ __launch_bounds__(256) void chunk_transpose_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                              int N, int K, int dir) {
+    const int n = blockIdx.y * 64 + (threadIdx.x & 63);
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kg = K >> 4;
+    if (n >= N || i >= kg) return;
+    const int64_t row_major = (static_cast<int64_t>(n) * kg + i) * 16;
+    const int64_t packed = (static_cast<int64_t>(i) * N + n) * 16;
+    if (dir == 0) *reinterpret_cast<uint4*>(dst + packed) = *reinterpret_cast<const uint4*>(src + row_major);
+    else *reinterpret_cast<uint4*>(dst + row_major) = *reinterpret_cast<const uint4*>(src + packed);
+}
+
+// (K, N) bytes -> (K/16, N, 16): P[i, n, j] = B[16 i + j, n]. One thread per
+// (i, 4 columns): 16 row loads of 4 bytes, a byte transpose in registers, one
+// 64-byte contiguous write.
+__global__ __launch_bounds__(256) void prepack_kn_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         int K, int N) {
+    const int n4 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const int i = blockIdx.y;
+    if (n4 >= N) return;
+    uint32_t r[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        r[j] = *reinterpret_cast<const uint32_t*>(src + static_cast<int64_t>(16 * i + j) * N + n4);
+    uint4 o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            w[q] = ((r[4 * q] >> (8 * c)) & 0xffu) | (((r[4 * q + 1] >> (8 * c)) & 0xffu) << 8) |
+                   (((r[4 * q + 2] >> (8 * c)) & 0xffu) << 16) | (((r[4 * q + 3] >> (8 * c)) & 0xffu) << 24);
+        }
+        o[c] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    uint4* d = reinterpret_cast<uint4*>(dst + (static_cast<int64_t>(i) * N + n4) * 16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) d[c] = o[c];
+}
+
+// Any N: one thread per output byte.
+__global__ __launch_bounds__(256) void prepack_kn_bytes_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                               int K, int N) {
+    const int64_t total = static_cast<int64_t>(K) * N;
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t j = o & 15;
+        const int64_t n = (o >> 4) % N;
+        const int64_t i = (o >> 4) / N;
+        dst[o] = src[(16 * i + j) * N + n];
+    }
+}
+
+// bf16 -> fp16 with round-toward-zero (v_cvt_pkrtz_f16_f32): values beyond
+// the fp16 range saturate to +-65504, inf stays inf, NaN stays NaN.
+__global__ __launch_bounds__(256) void bf16_to_fp16_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
+                                                           int64_t n) {
+    const int64_t nvec = n / 8;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < nvec; g += stride) {
+        const uint4 t = reinterpret_cast<const uint4*>(in)[g];
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float lo = bits_f32(w[h] << 16);
+            const float hi = bits_f32(w[h] & 0xffff0000u);
+            o[h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+        }
+        reinterpret_cast<uint4*>(out)[g] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+        const int64_t e = nvec * 8 + threadIdx.x;
+        const float f = bits_f32(static_cast<uint32_t>(in[e]) << 16);
+        out[e] = static_cast<uint16_t>(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f, 0.0f)) & 0xffffu);
+    }
+}
+
+// dequantize (K/16, N, 16) e5m2 -> (N, K) in dtype T: T(float32(q) * s),
+// following quant.py:99-102 (FeatherFP8E5M2PackedLayout.dequantize).
+template <int DT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ src, const float* __restrict__ scale,
+                                                      void* __restrict__ dst, int N, int K) {
+    const int n = blockIdx.y * 64 + (threadIdx.x & 63);
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N || i >= (K >> 4)) return;
+    const float s = scale[0];
+    const uint4 raw = *reinterpret_cast<const uint4*>(src + (static_cast<int64_t>(i) * N + n) * 16);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint16_t h = static_cast<uint16_t>(((w[j >> 2] >> (8 * (j & 3))) & 0xffu) << 8);
+        v[j] = half_bits_to_f32(h) * s;
+    }
+    const int64_t base = static_cast<int64_t>(n) * K + i * 16;
+    if constexpr (DT == kDtypeF32) {
+        float4* d = reinterpret_cast<float4*>(static_cast<float*>(dst) + base);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    } else {
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t lo, hi;
+            if constexpr (DT == kDtypeF16) { lo = f32_to_half_bits(v[2 * j]); hi = f32_to_half_bits(v[2 * j + 1]); }
+            else { lo = f32_to_bf16_bits(v[2 * j]); hi = f32_to_bf16_bits(v[2 * j + 1]); }
+            o[j] = lo | (hi << 16);
+        }
+        uint4* d = reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst) + base);
+        d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+}
+
+int grid_for(int64_t work, int per_block, int cap) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return static_cast<int>(g);
+}
+
+template <int DT>
+void launch_quant(const QuantArgs& q, hipStream_t stream) {
+    const int64_t n = q.N * q.K;
+    const bool premul = !q.native;
+    if (!q.scale_in) {
+        hipLaunchKernelGGL(zero_word_kernel, dim3(1), dim3(1), 0, stream, q.workspace);
+        hipLaunchKernelGGL((amax_kernel<DT>), dim3(grid_for(n / 16, 256, 4096)), dim3(256), 0, stream, q.w, n,
+                           q.ckpt_scale, premul ? 1 : 0, q.workspace);
+    }
+    const dim3 grid(static_cast<uint32_t>((q.K / 16 + 3) / 4), static_cast<uint32_t>((q.N + 63) / 64));
+    hipLaunchKernelGGL((quant_prepack_kernel<DT>), grid, dim3(256), 0, stream, q.w, static_cast<int>(q.N),
+                       static_cast<int>(q.K), q.ckpt_scale, q.native ? 1 : 0, q.workspace, q.scale_in, q.out,
+                       q.scale_out);
+}
+
+}  // namespace
+
+void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream) {
+    switch (q.dtype) {
+        case kDtypeF16: launch_quant<kDtypeF16>(q, stream); break;
+        case kDtypeBF16: launch_quant<kDtypeBF16>(q, stream); break;
+        default: launch_quant<kDtypeF32>(q, stream); break;
+    }
+}
+
+void launch_chunk_transpose(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int dir, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>((K / 16 + 3) / 4), static_cast<uint32_t>((N + 63) / 64));
+    hipLaunchKernelGGL(chunk_transpose_kernel, grid, dim3(256), 0, stream, src, dst, static_cast<int>(N),
+                       static_cast<int>(K), dir);
+}
+
+void launch_prepack_kn(const uint8_t* src, uint8_t* dst, int64_t K, int64_t N, hipStream_t stream) {
+    if (N % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 3u) == 0) {
+        const dim3 grid(static_cast<uint32_t>((N / 4 + 255) / 256), static_cast<uint32_t>(K / 16));
+        hipLaunchKernelGGL(prepack_kn_kernel, grid, dim3(256), 0, stream, src, dst, static_cast<int>(K),
+                           static_cast<int>(N));
+    } else {
+        hipLaunchKernelGGL(prepack_kn_bytes_kernel, dim3(grid_for(K * N, 256, 8192)), dim3(256), 0, stream, src, dst,
+                           static_cast<int>(K), static_cast<int>(N));
+    }
+}
+
+void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(bf16_to_fp16_kernel, dim3(grid_for(n / 8, 256, 8192)), dim3(256), 0, stream, in, out, n);
+}
+
+void launch_dequant(const uint8_t* src, const float* scale, void* dst, int64_t N, int64_t K, int dtype,
+                    hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>((K / 16 + 3) / 4), static_cast<uint32_t>((N + 63) / 64));
+    switch (dtype) {
+        case kDtypeF16:
+            hipLaunchKernelGGL((dequant_kernel<kDtypeF16>), grid, dim3(256), 0, stream, src, scale, dst,
+                               static_cast<int>(N), static_cast<int>(K));
+            break;
+        case kDtypeBF16:
+            hipLaunchKernelGGL((dequant_kernel<kDtypeBF16>), grid, dim3(256), 0, stream, src, scale, dst,
+                               static_cast<int>(N), static_cast<int>(K));
+            break;
+        default:
+            hipLaunchKernelGGL((dequant_kernel<kDtypeF32>), grid, dim3(256), 0, stream, src, scale, dst,
+                               static_cast<int>(N), static_cast<int>(K));
+            break;
+    }
+}
+
+}  // namespace feather

@@ -1,0 +1,39 @@
+// Host-side description of one scaled_mm call and the gfx950 kernel variants
+// that can serve it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace feather {
+
+struct MmArgs {
+    const uint16_t* a;       // (M, K) fp16, row-major
+    const uint8_t* b;        // (K/16, N, 16) fp8 bytes
+    const float* scale;      // device scalar, read when has_scale
+    const uint16_t* bias;    // (N,) in the output type, read when has_bias
+    uint16_t* c;             // (M, N) fp16 / bf16, row-major
+    int64_t M, N, K;
+    int has_scale, has_bias;
+    bool out_bf16;
+    bool b_e4m3;
+    int group_m;             // tile raster group height (0 = default)
+};
+
+// Kernel variants. Values are stable: the Python autotuner de-duplicates
+// reference configs by the id they map to.
+enum KernelId : int {
+    kKernelNone = 0,
+    kTile256x256 = 1,
+    kTile256x128 = 2,
+    kTile128x256 = 3,
+    kTile128x128 = 4,
+    kTile64x128 = 5,
+    kTile64x64 = 6,
+    kSmallM = 10,  // M <= 64: split-K inside the workgroup, one 16-column strip per workgroup
+};
+
+bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
+bool launch_smallm_kernel(const MmArgs& p, hipStream_t stream);
+
+}  // namespace feather

@@ -1,0 +1,245 @@
+"""Drop-in Python surface of the scaled_mm hot path (reference kernel/hip/hip_kernel.py).
+
+Public names and signatures are the reference's:
+    scaled_mm_hip(a, b_prepacked, scale, bias, out_dtype)              (:136-167)
+    scaled_mm_hip_configured(a, b_prepacked, scale, bias, out_dtype,
+                             block_warps_m, block_warps_n, unroll_k,
+                             repeat_m, repeat_n)                        (:12-58)
+    prepack_b_for_scaled_mm(b)                                          (:170-171)
+    _CONFIGS                                                            (:60-91)
+plus the native op `torch.ops.feather_ops.scaled_mm` with the reference
+schema (hip_kernel.cu:746-767) and its validation (hip_kernel.cu:648-730).
+
+The native op calls `launch_scaled_mm` of libfeatherops_amd.so through
+ctypes on torch's current stream; there is no other compute path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .utils import generate_autotune_configs, get_compatible_config, old_autotune
+
+# ---------------------------------------------------------------------------
+# validation (hip_kernel.cu:648-730), usable without a GPU for host-side tests
+# ---------------------------------------------------------------------------
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
+                       b_dtype, require_cuda: bool = True) -> None:
+    """Raise RuntimeError with the reference's message for any argument the
+    kernel cannot take. `require_cuda=False` skips the device checks."""
+    if require_cuda:
+        _check(a.is_cuda, "a must be a CUDA tensor")
+        _check(b_prepacked.is_cuda, "b_prepacked must be a CUDA tensor")
+        _check(c.is_cuda, "c must be a CUDA tensor")
+        _check(b_prepacked.device == a.device, "b_prepacked must be on the same device as a")
+        _check(c.device == a.device, "c must be on the same device as a")
+    _check(a.dtype == torch.float16, "a must be float16")
+    _check(c.dtype in (torch.float16, torch.bfloat16), "c must be float16 or bfloat16")
+    _check(b_dtype in (0, 1), "b_dtype must be 0 (fp8e4m3) or 1 (fp8e5m2)")
+    if b_dtype == 0:
+        _check(b_prepacked.dtype == torch.float8_e4m3fn, "b_prepacked must be float8_e4m3fn when b_dtype=0")
+    else:
+        _check(b_prepacked.dtype == torch.float8_e5m2, "b_prepacked must be float8_e5m2 when b_dtype=1")
+    _check(a.dim() == 2, "a must be 2D")
+    _check(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)")
+    _check(c.dim() == 2, "c must be 2D")
+    M, K = a.shape
+    N = b_prepacked.shape[1]
+    _check(K % 16 == 0, "K must be divisible by 16")
+    _check(b_prepacked.shape[0] == K // 16, f"b_prepacked.shape[0] must equal K/16 ({K // 16})")
+    _check(b_prepacked.shape[2] == 16, "b_prepacked.shape[2] must be 16")
+    _check(c.shape[0] == M, "c.shape[0] must equal M")
+    _check(c.shape[1] == N, "c.shape[1] must equal N")
+    _check(a.stride(0) == K, f"a.stride(0) must equal K ({K})")
+    _check(a.stride(1) == 1, "a.stride(1) must be 1")
+    _check(b_prepacked.stride(0) == N * 16, f"b_prepacked.stride(0) must equal N*16 ({N * 16})")
+    _check(b_prepacked.stride(1) == 16, "b_prepacked.stride(1) must be 16")
+    _check(b_prepacked.stride(2) == 1, "b_prepacked.stride(2) must be 1")
+    _check(c.stride(0) == N, f"c.stride(0) must equal N ({N})")
+    _check(c.stride(1) == 1, "c.stride(1) must be 1")
+    if scale is not None:
+        if require_cuda:
+            _check(scale.is_cuda, "scale must be a CUDA tensor")
+            _check(scale.device == a.device, "scale must be on the same device as a")
+        _check(scale.dtype == torch.float32, "scale must be float32")
+        _check(scale.numel() == 1, "scale must have one element")
+    if bias is not None:
+        if require_cuda:
+            _check(bias.is_cuda, "bias must be a CUDA tensor")
+            _check(bias.device == a.device, "bias must be on the same device as a")
+        _check(bias.dtype == c.dtype, "bias must have the same dtype as c")
+        _check(bias.numel() == N, "bias must have N elements")
+    if require_cuda:
+        for name, t in (("a", a), ("b_prepacked", b_prepacked), ("c", c)):
+            _check(t.data_ptr() % 16 == 0, f"{name} data pointer must be 16-byte aligned")
+    block_m = 16 * block_warps_m * repeat_m
+    block_n = 16 * block_warps_n * repeat_n
+    chunk_k = 16 * unroll_k
+    _check(M % block_m == 0, f"M ({M}) must be divisible by kBlockM ({block_m})")
+    _check(N % block_n == 0, f"N ({N}) must be divisible by kBlockN ({block_n})")
+    _check(K % chunk_k == 0, f"K ({K}) must be divisible by kChunkK ({chunk_k})")
+    _check(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit")
+
+
+def _scaled_mm_native(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
+                      b_dtype) -> None:
+    validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
+                       b_dtype)
+    L = _lib.lib()
+    dev = a.device
+    with torch.cuda.device(dev):
+        launched = L.launch_scaled_mm(
+            a.data_ptr(), b_prepacked.data_ptr(),
+            scale.data_ptr() if scale is not None else None,
+            bias.data_ptr() if bias is not None else None,
+            c.data_ptr(), a.shape[0], b_prepacked.shape[1], a.shape[1],
+            1 if scale is not None else 0, 1 if bias is not None else 0,
+            block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
+            0 if c.dtype == torch.float16 else 1, _lib.stream_ptr(dev))
+    _check(bool(launched), "Unsupported config")
+
+
+# torch op feather_ops::scaled_mm with the reference schema (hip_kernel.cu:746-767)
+_SCHEMA = ("scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, "
+           "int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype) -> ()")
+if not hasattr(torch.ops, "feather_ops") or not hasattr(torch.ops.feather_ops, "scaled_mm"):
+    _LIB_DEF = torch.library.Library("feather_ops", "DEF")
+    _LIB_DEF.define(_SCHEMA)
+    _LIB_CUDA = torch.library.Library("feather_ops", "IMPL", "CUDA")
+    _LIB_CUDA.impl("scaled_mm", _scaled_mm_native)
+
+
+def kernel_id(M: int, N: int, K: int, cfg) -> int:
+    """gfx950 kernel a config runs for this shape (0 = unsupported)."""
+    return int(_lib.lib().feather_scaled_mm_kernel_id(M, N, K, *cfg))
+
+
+# ---------------------------------------------------------------------------
+# torch.library custom ops (hip_kernel.py:12-133)
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("feather_ops_internal::scaled_mm_configured", mutates_args=())
+def _configured_op(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+    block_warps_m: int,
+    block_warps_n: int,
+    unroll_k: int,
+    repeat_m: int,
+    repeat_n: int,
+) -> torch.Tensor:
+    out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+    torch.ops.feather_ops.scaled_mm.default(
+        a, b_prepacked, scale, bias, out, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
+        0 if b_prepacked.dtype == torch.float8_e4m3fn else 1,
+    )
+    return out
+
+
+@_configured_op.register_fake
+def _(a, b_prepacked, scale, bias, out_dtype, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n):
+    return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+
+
+scaled_mm_hip_configured = _configured_op
+
+# Reference configurations (hip_kernel.py:60-89), then two gfx950 tiles:
+# (2,4,4,8,4) -> 256x256 and (4,2,4,4,4) -> 256x128 output tiles.
+_CONFIGS = [
+    (1, 1, 2, 1, 2), (1, 1, 4, 1, 2), (1, 2, 2, 1, 2), (1, 2, 4, 1, 2), (1, 4, 2, 1, 2), (1, 4, 4, 1, 2),
+    (1, 8, 2, 1, 2), (1, 8, 4, 1, 2), (1, 1, 2, 2, 2), (1, 1, 4, 2, 2), (1, 1, 2, 4, 4), (1, 1, 4, 4, 4),
+    (1, 2, 2, 2, 2), (1, 2, 4, 2, 2), (2, 1, 2, 2, 2), (2, 1, 4, 2, 2), (1, 4, 2, 4, 2), (1, 4, 4, 4, 2),
+    (1, 8, 2, 8, 2), (1, 8, 4, 8, 2), (2, 2, 2, 4, 4), (2, 2, 4, 4, 4), (2, 4, 2, 4, 2), (2, 4, 4, 4, 2),
+    (2, 4, 2, 4, 4), (2, 4, 4, 4, 4), (4, 2, 2, 2, 4), (4, 2, 4, 2, 4),
+    (2, 4, 4, 8, 4), (4, 2, 4, 4, 4),
+]
+_CONFIGS = sorted(_CONFIGS, key=lambda x: (x[0], x[1], x[3], x[4], x[2]))
+
+
+@torch.library.custom_op("feather_ops_internal::scaled_mm_autotuned", mutates_args=())
+def _autotuned_op(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor,
+    bias: torch.Tensor,
+    out_dtype: torch.dtype,
+    has_scale: bool,
+    has_bias: bool,
+    block_warps_m: int = 0,
+    block_warps_n: int = 0,
+    unroll_k: int = 0,
+    repeat_m: int = 0,
+    repeat_n: int = 0,
+) -> torch.Tensor:
+    if min(block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n) <= 0:
+        block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n = get_compatible_config(a, b_prepacked, 1, _CONFIGS)
+    return _configured_op(a, b_prepacked, scale if has_scale else None, bias if has_bias else None, out_dtype,
+                          block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n)
+
+
+@_autotuned_op.register_fake
+def _(a, b_prepacked, scale, bias, out_dtype, has_scale, has_bias, block_warps_m=0, block_warps_n=0, unroll_k=0,
+      repeat_m=0, repeat_n=0):
+    return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+
+
+try:
+    from torch._inductor.kernel.custom_op import register_custom_op_autotuning
+
+    register_custom_op_autotuning(
+        _autotuned_op, config_generator=lambda fake_tensors: generate_autotune_configs(fake_tensors, _CONFIGS, 1))
+except ImportError:  # inductor without custom-op autotuning: compile still uses the default config
+    pass
+
+
+def scaled_mm_hip(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """Autotuned entry (hip_kernel.py:136-167)."""
+    if torch.compiler.is_compiling():
+        return _autotuned_op(a, b_prepacked, scale if scale is not None else a, bias if bias is not None else a,
+                             out_dtype, scale is not None, bias is not None)
+
+    def run_fn(cfg):
+        return _configured_op(a, b_prepacked, scale, bias, out_dtype, *cfg)
+
+    M, K = a.shape[0], a.shape[1]
+    N = b_prepacked.shape[1]
+    best_cfg = old_autotune(M, N, K, _CONFIGS, run_fn, "mixed", b_prepacked.dtype, out_dtype,
+                            kernel_id=lambda cfg: kernel_id(M, N, K, cfg))
+    return _configured_op(a, b_prepacked, scale, bias, out_dtype, *best_cfg)
+
+
+def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
+    """(K, N) -> (K/16, N, 16) (hip_kernel.py:170-171), on the GPU.
+
+    Any 1-byte dtype works (fp8 weights are the use); a CPU tensor is moved to
+    the current GPU, repacked there and returned on its own device."""
+    if b.dim() != 2 or b.element_size() != 1:
+        raise ValueError(f"prepack_b_for_scaled_mm expects a 2-D 1-byte tensor, got {tuple(b.shape)} {b.dtype}")
+    K, N = b.shape
+    if K % 16 != 0:
+        raise ValueError(f"K ({K}) must be divisible by 16")
+    src = b if b.is_cuda else b.to("cuda")
+    src = src.contiguous()
+    out = torch.empty((K // 16, N, 16), dtype=b.dtype, device=src.device)
+    with torch.cuda.device(src.device):
+        _lib.check(_lib.lib().feather_prepack_b(src.data_ptr(), out.data_ptr(), K, N, _lib.stream_ptr(src.device)),
+                   "prepack_b_for_scaled_mm")
+    return out if b.is_cuda else out.to(b.device)

@@ -1,0 +1,124 @@
+/*
+ * featherops_amd -- C ABI of the MI355X (gfx950) FeatherOps hot path.
+ *
+ * libfeatherops_amd.so exports these symbols with C linkage. Every pointer is
+ * device memory owned by the caller; no entry point allocates, synchronises
+ * or keeps state between calls. All work is enqueued asynchronously on
+ * `stream`.
+ *
+ * Tensor layouts:
+ *   A            (M, K)        fp16, row-major, 16-byte aligned
+ *   b_prepacked  (K/16, N, 16) fp8 bytes (e5m2 or e4m3fn), 16-byte aligned:
+ *                element (k, n) of the (K, N) weight is at [k/16][n][k%16]
+ *   C            (M, N)        fp16 or bf16, row-major, 16-byte aligned
+ *   bias         (N,)          same type as C
+ *   scale        one fp32 on the device (read by the kernel, no host sync)
+ */
+#ifndef FEATHEROPS_AMD_H
+#define FEATHEROPS_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes of the int-returning entry points. */
+#define FEATHER_OK 0
+#define FEATHER_ERR_INVALID 1      /* argument out of the supported domain */
+#define FEATHER_ERR_UNSUPPORTED 2  /* no kernel for this configuration */
+#define FEATHER_ERR_LAUNCH 3       /* hipGetLastError() reported a launch failure */
+
+/* Data type codes. */
+#define FEATHER_DTYPE_F16 0
+#define FEATHER_DTYPE_BF16 1
+#define FEATHER_DTYPE_F32 2
+#define FEATHER_B_E4M3FN 0
+#define FEATHER_B_E5M2 1
+
+/*
+ * C = out( out(A @ dec(b_prepacked) * scale) + bias ), fp32 accumulation.
+ * Replaces `extern "C" bool launch_scaled_mm(...)` of the reference,
+ * kernel/hip/hip_kernel.cu:564-632 (same argument order and meaning; `a` is
+ * the fp16 A pointer the reference types as `const half*`).
+ *   has_scale / has_bias: 0 or 1; scale / bias are only read when set.
+ *   (block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n): one of the
+ *   configurations the reference lists (hip_kernel.py:60-89) or one of the
+ *   gfx950 additions (2,4,4,8,4), (4,2,4,4,4). The tuple keeps the reference's
+ *   divisibility meaning (BlockM = 16*wm*rm, BlockN = 16*wn*rn, ChunkK = 16*u)
+ *   for callers that pad to it; the kernels themselves accept any M.
+ *   b_dtype: FEATHER_B_E4M3FN or FEATHER_B_E5M2. output_dtype: 0 fp16, 1 bf16.
+ * Returns false (and launches nothing) for a configuration outside that list,
+ * N or K not a multiple of 16, or sizes beyond int32; like the reference it
+ * does not call hipGetLastError itself.
+ */
+bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                      uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias, int block_warps_m,
+                      int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype, int output_dtype,
+                      hipStream_t stream);
+
+/*
+ * Which gfx950 kernel launch_scaled_mm would run for this shape and
+ * configuration (0 = unsupported configuration). Several reference
+ * configurations map onto one kernel; the autotuner
+ * (kernel/hip/utils.py:192-223 in the reference) times each kernel once.
+ * No counterpart in the reference.
+ */
+int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n, int unroll_k,
+                                int repeat_m, int repeat_n);
+
+/*
+ * Quantize an (N, K) weight to fp8 e5m2 with a per-tensor scale and write it
+ * prepacked as (K/16, N, 16). Replaces the torch arithmetic of
+ * comfy_feather/quant.py:52-74 followed by prepack_transpose (quant.py:11-13):
+ *   native = 0: load path, make_feather_quantized_weight (quant.py:116-136):
+ *               fp32 arithmetic on w * ckpt_scale (ckpt_scale may be NULL = 1)
+ *   native = 1: patch path, quantize_feather_weight (quant.py:139-146):
+ *               arithmetic in w's dtype, fp16 reciprocal clamp (quant.py:56-58)
+ * w_dtype: FEATHER_DTYPE_F16 / _BF16 / _F32. K % 16 == 0, w 16-byte aligned.
+ * scale_out receives the fp32 scale. workspace: >= 4 bytes of device memory,
+ * overwritten (cleared by a kernel, no hipMemset). Returns a status code.
+ */
+int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,
+                                  int native, uint8_t* out, float* scale_out, uint32_t* workspace, hipStream_t stream);
+
+/*
+ * Same output with a caller-given scale (no amax, no clamp): q = e5m2(w *
+ * T(1/scale)) in w's dtype T. Replaces quant.py:59-74 when `scale` is passed
+ * to quantize_fp8e5m2_scaled. No workspace.
+ */
+int feather_quantize_prepack_e5m2_scaled(const void* w, int w_dtype, int64_t N, int64_t K, const float* scale,
+                                         uint8_t* out, hipStream_t stream);
+
+/* (N, K) bytes -> (K/16, N, 16). Replaces quant.py:11-13 (prepack_transpose). */
+int feather_prepack_transpose(const uint8_t* w_nk, uint8_t* out, int64_t N, int64_t K, hipStream_t stream);
+
+/* (K/16, N, 16) -> (N, K) bytes. Replaces quant.py:17-19 (unprepack_transpose). */
+int feather_unprepack_transpose(const uint8_t* packed, uint8_t* out_nk, int64_t N, int64_t K, hipStream_t stream);
+
+/* (K, N) bytes -> (K/16, N, 16). Replaces kernel/hip/hip_kernel.py:170-171
+ * (prepack_b_for_scaled_mm). */
+int feather_prepack_b(const uint8_t* b_kn, uint8_t* out, int64_t K, int64_t N, hipStream_t stream);
+
+/* bf16 -> fp16, round toward zero (saturating). Replaces kernel/convert.py:6-34
+ * (bf16_to_fp16); n may be any count, buffers 16-byte aligned. */
+int feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+
+/* (K/16, N, 16) e5m2 -> (N, K) of out_dtype as out_dtype(float32(q) * scale).
+ * Replaces quant.py:99-102 (FeatherFP8E5M2PackedLayout.dequantize). */
+int feather_dequantize_e5m2(const uint8_t* packed, const float* scale, void* out, int out_dtype, int64_t N, int64_t K,
+                            hipStream_t stream);
+
+/* Text for a status code. */
+const char* feather_status_string(int status);
+
+/* ABI revision of this header (bumped on any signature change). */
+int feather_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FEATHEROPS_AMD_H */

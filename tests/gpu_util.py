@@ -1,0 +1,84 @@
+"""Helpers shared by the GPU parity tests: C-ABI calls and the output gate."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import feather_oracle as O
+
+
+def lib():
+    from featherops_amd.kernel.hip import _lib
+
+    return _lib.lib()
+
+
+def stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def capi_scaled_mm(a, bp, scale, bias, out_dtype, cfg=(2, 4, 4, 8, 4), b_dtype=1):
+    """Run launch_scaled_mm through the C ABI on device tensors; returns C."""
+    M, K = a.shape
+    N = bp.shape[1]
+    c = torch.full((M, N), float("nan"), dtype=out_dtype, device=a.device)
+    ok = lib().launch_scaled_mm(
+        a.data_ptr(), bp.data_ptr(), scale.data_ptr() if scale is not None else None,
+        bias.data_ptr() if bias is not None else None, c.data_ptr(), M, N, K,
+        int(scale is not None), int(bias is not None), *cfg, b_dtype,
+        0 if out_dtype == torch.float16 else 1, stream(a.device))
+    assert ok, f"launch_scaled_mm refused cfg={cfg} M={M} N={N} K={K}"
+    torch.cuda.synchronize()
+    return c
+
+
+def out_to_f32(y) -> np.ndarray:
+    """Kernel output tensor or oracle array (float16 / bf16 bits) -> float32 numpy."""
+    if isinstance(y, torch.Tensor):
+        return y.float().cpu().numpy()
+    if y.dtype == np.uint16:
+        return O.bf16_bits_to_f32(y)
+    return y.astype(np.float32)
+
+
+def _ulp(x: np.ndarray, mant_bits: int) -> np.ndarray:
+    ax = np.maximum(np.abs(x.astype(np.float64)), 2.0**-14)
+    return 2.0 ** (np.floor(np.log2(ax)) - mant_bits)
+
+
+def assert_gemm_close(out, ref, out_dtype, label=""):
+    """Parity gate against the oracle (both rounded to the output type).
+
+    rel-Frobenius <= 1e-3 and every element within max(2e-2, 1 ulp of the
+    output type at |ref|): the kernel's fp32 sums run in a different order than
+    the oracle's float64 sum, which can move a result across one rounding
+    boundary of the output type (for bf16 above |y| = 2.56, and for fp16 above
+    |y| = 20.48, one ulp exceeds 2e-2). Non-finite values must agree exactly."""
+    o = out_to_f32(out)
+    r = out_to_f32(ref)
+    fin = np.isfinite(r)
+    assert np.array_equal(np.isnan(o), np.isnan(r)), f"{label}: NaN pattern differs"
+    assert np.array_equal(o[np.isinf(r)], r[np.isinf(r)]), f"{label}: inf pattern differs"
+    d = np.abs(o[fin].astype(np.float64) - r[fin])
+    mant = 10 if out_dtype == torch.float16 else 7
+    tol = np.maximum(2e-2, _ulp(r[fin], mant) * 1.0001)
+    fro = np.linalg.norm(d) / max(np.linalg.norm(r[fin]), 1e-6)
+    worst = float((d / tol).max()) if d.size else 0.0
+    assert fro <= 1e-3, f"{label}: rel-Fro {fro:.3g} > 1e-3"
+    assert worst <= 1.0, f"{label}: max |diff|/tol = {worst:.3g} (max abs {d.max():.3g})"
+    return float(d.max()) if d.size else 0.0, float(fro)
+
+
+def weight_like(N, K, gen, std=0.02):
+    """~N(0, std) weight with a per-tensor e5m2 scale amax/57344: ((K/16,N,16) codes, scale).
+    Test data only (torch's CPU cast, which the oracle's encoder is pinned to)."""
+    w = torch.randn(N, K, generator=gen) * std
+    s = np.float32(w.abs().max().item()) / np.float32(57344.0)
+    codes = (w * float(np.float32(1.0) / s)).to(torch.float8_e5m2).view(torch.uint8)
+    packed = codes.view(N, K // 16, 16).permute(1, 0, 2).contiguous().numpy()
+    return packed, np.float32(s)
+
+
+def to_dev_codes(packed: np.ndarray, dev, dtype=torch.float8_e5m2):
+    return torch.from_numpy(np.ascontiguousarray(packed)).view(dtype).to(dev)

@@ -1,0 +1,110 @@
+"""GPU tests of the drop-in callers: FeatherOps.Linear, scaled_mm_hip autotune,
+and the torch.compile contract (reference test_scaled_mm_hip_autotune_compile.py)."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_gemm_close
+from oracle import feather_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear_ref(x: torch.Tensor, qdata: torch.Tensor, scale: float, bias, out_dtype):
+    a = x.reshape(-1, x.shape[-1]).to(torch.float16).cpu().numpy()
+    od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+    b = None
+    if bias is not None:
+        b = bias.cpu().numpy() if out_dtype == torch.float16 else bias.cpu().view(torch.int16).numpy().view(np.uint16)
+    return O.scaled_mm_ref(a, qdata.view(torch.uint8).cpu().numpy(), np.float32(scale), b, od)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 37, 130, 300])
+def test_feather_linear_forward(cuda, pkg, out_dtype, m):
+    from featherops_amd.comfy_feather import ops, quant
+
+    g = torch.Generator().manual_seed(m)
+    K, N = 256, 384
+    ops_cls = ops.feather_ops(out_dtype=out_dtype)
+    lin = ops_cls.Linear(K, N)
+    sd = {"weight": (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16),
+          "bias": (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)}
+    lin._load_from_state_dict(sd, "", {}, True, [], [], [])
+    assert lin.is_quantized
+    lin.weight = lin.weight.to(cuda) if not isinstance(lin.weight, torch.Tensor) else lin.weight
+    lin.bias = torch.nn.Parameter(lin.bias.to(cuda), requires_grad=False)
+    qdata, scale = quant.get_feather_plain_tensors(lin.weight)
+    x = torch.randn(2, m, K, generator=g).to(torch.bfloat16).to(cuda)
+    y = lin(x)
+    torch.cuda.synchronize()
+    assert y.shape == (2, m, N) and y.dtype == torch.bfloat16
+    ref = _linear_ref(x, qdata, scale.item(), lin.bias, out_dtype)
+    # the layer casts its out_dtype result back to the input dtype (bf16)
+    ref_t = torch.from_numpy(O.bf16_bits_to_f32(ref) if ref.dtype == np.uint16 else ref.astype(np.float32))
+    ref_bf = ref_t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_gemm_close(y.reshape(-1, N), ref_bf, torch.bfloat16, f"linear m={m}")
+
+
+def test_feather_linear_excluded_and_patch(cuda, pkg):
+    from featherops_amd.comfy_feather import ops, quant
+
+    ops_cls = ops.feather_ops(out_dtype=torch.float16, excluded_names=("proj_out",))
+    lin = ops_cls.Linear(64, 32)
+    w = torch.randn(32, 64) * 0.1
+    lin._load_from_state_dict({"weight": w.clone()}, "proj_out.", {}, True, [], [], [])
+    assert not lin.is_quantized
+    lin2 = ops_cls.Linear(64, 32)
+    lin2._load_from_state_dict({"weight": w.clone().to(cuda)}, "blocks.0.", {}, True, [], [], [])
+    assert lin2.is_quantized
+    deq = lin2.convert_weight(lin2.weight)
+    assert deq.shape == (32, 64) and deq.dtype == torch.float16
+    assert (deq.float().cpu() - w).abs().max().item() <= w.abs().max().item() * 2**-3
+    lin2.set_weight(deq)
+    assert quant.is_feather_quantized_weight(lin2.weight)
+    y = lin2(torch.zeros(0, 64, device=cuda))
+    assert y.shape == (0, 32)
+
+
+def test_scaled_mm_hip_autotune_eager(cuda, hk):
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(512, 512, generator=g).half()
+    b = torch.randn(512, 512, generator=g).to(torch.float8_e5m2)
+    bias = torch.randn(512, generator=g).half()
+    bp = hk.prepack_b_for_scaled_mm(b.to(cuda))
+    s = torch.tensor(2.34, device=cuda)
+    y = hk.scaled_mm_hip(a.to(cuda), bp, s, bias.to(cuda), torch.float16)
+    ref = O.scaled_mm_ref(a.numpy(), bp.view(torch.uint8).cpu().numpy(), np.float32(2.34), bias.numpy(), O.DT_F16)
+    assert_gemm_close(y, ref, torch.float16, "autotuned")
+    y2 = hk.scaled_mm_hip(a.to(cuda), bp, None, None, torch.float16)  # no scale, no bias
+    ref2 = O.scaled_mm_ref(a.numpy(), bp.view(torch.uint8).cpu().numpy(), None, None, O.DT_F16)
+    assert_gemm_close(y2, ref2, torch.float16, "autotuned no scale")
+
+
+def test_torch_compile_configured_and_autotuned(cuda, hk):
+    g = torch.Generator().manual_seed(1)
+    a = torch.randn(512, 512, generator=g).half().to(cuda)
+    b = torch.randn(512, 512, generator=g).to(torch.float8_e5m2)
+    bias = torch.randn(512, generator=g).half().to(cuda)
+    bp = hk.prepack_b_for_scaled_mm(b.to(cuda))
+    s = torch.tensor(2.34, device=cuda)
+    ref = O.scaled_mm_ref(a.cpu().numpy(), bp.view(torch.uint8).cpu().numpy(), np.float32(2.34),
+                          bias.cpu().numpy(), O.DT_F16)
+
+    @torch.compile(fullgraph=True)
+    def configured(a, bp, s, bias):
+        return hk.scaled_mm_hip_configured(a, bp, s, bias, torch.float16, 1, 1, 2, 1, 2)
+
+    assert_gemm_close(configured(a, bp, s, bias), ref, torch.float16, "compile configured")
+
+    @torch.compile(fullgraph=True)
+    def autotuned(x, bp, bias):
+        x = x.to(torch.float16).view(-1, x.shape[-1])
+        return hk.scaled_mm_hip(x, bp, None, bias, torch.float16)
+
+    xv = a.view(2, 256, 512).to(torch.bfloat16)
+    y = autotuned(xv, bp, bias)
+    ref2 = O.scaled_mm_ref(xv.to(torch.float16).view(-1, 512).cpu().numpy(), bp.view(torch.uint8).cpu().numpy(),
+                           None, bias.cpu().numpy(), O.DT_F16)
+    assert_gemm_close(y, ref2, torch.float16, "compile autotuned view input no scale")

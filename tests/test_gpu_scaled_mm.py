@@ -1,0 +1,176 @@
+"""GPU parity of the scaled_mm kernels against the oracle (through the C ABI
+and the drop-in Python API)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from gpu_util import assert_gemm_close, capi_scaled_mm, to_dev_codes, weight_like
+from oracle import feather_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TILE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 4), (2, 4, 4, 4, 4), (4, 2, 4, 2, 4), (1, 8, 4, 4, 2), (1, 1, 2, 2, 2)]
+
+
+def _bias_for(out_dtype, n, gen):
+    b16 = (torch.randn(n, generator=gen) * 0.01).half()
+    if out_dtype == torch.float16:
+        return b16, b16.numpy()
+    bb = b16.float().bfloat16()
+    return bb, bb.view(torch.int16).numpy().view(np.uint16)
+
+
+def test_golden_small_all_kernels(cuda, hk):
+    z = np.load(GOLDEN / "gemm_small.npz")
+    a = torch.from_numpy(z["a"]).to(cuda)
+    bp = to_dev_codes(z["b_prepacked"], cuda)
+    s = torch.from_numpy(z["scale"]).to(cuda)
+    b16 = torch.from_numpy(z["bias_f16"]).to(cuda)
+    bbf = torch.from_numpy(z["bias_bf16"].view(np.int16)).view(torch.bfloat16).to(cuda)
+    for cfg in hk._CONFIGS:
+        print("golden cfg", cfg, flush=True)
+        y = capi_scaled_mm(a, bp, s, b16, torch.float16, cfg)
+        assert_gemm_close(y, z["out_f16"], torch.float16, f"f16 {cfg}")
+        y = capi_scaled_mm(a, bp, s, bbf, torch.bfloat16, cfg)
+        assert_gemm_close(y, z["out_bf16"], torch.bfloat16, f"bf16 {cfg}")
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 128, 128), (48, 256, 1024), (64, 512, 4096), (128, 128, 128),
+                                   (256, 256, 512), (512, 256, 256), (100, 384, 320), (300, 512, 1040),
+                                   (1024, 1024, 1024)])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_shapes_and_tiles(cuda, M, N, K, out_dtype):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    a = torch.randn(M, K, generator=g).half()
+    packed, s = weight_like(N, K, g)
+    bias, bias_np = _bias_for(out_dtype, N, g)
+    od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+    ref = O.scaled_mm_ref(a.numpy(), packed, s, bias_np, od)
+    ad, bd = a.to(cuda), to_dev_codes(packed, cuda)
+    sd = torch.tensor([s], device=cuda)
+    for cfg in TILE_CFGS:
+        print("shape", M, N, K, out_dtype, cfg, flush=True)
+        y = capi_scaled_mm(ad, bd, sd, bias.to(cuda), out_dtype, cfg)
+        assert_gemm_close(y, ref, out_dtype, f"{M}x{N}x{K} {cfg}")
+
+
+@pytest.mark.parametrize("b_dtype", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_reference_style_inputs(cuda, hk, b_dtype, out_dtype):
+    """The reference test's data (test_scaled_mm_hip.py:10-13): B = randn cast to
+    fp8, scale 2.34, bias randn in the output type, every compatible config."""
+    g = torch.Generator().manual_seed(11)
+    for M, N, K in [(16, 128, 128), (256, 256, 256), (512, 512, 512)]:
+        a = torch.randn(M, K, generator=g).half()
+        b = torch.randn(K, N, generator=g).to(b_dtype)
+        bias = torch.randn(N, generator=g).to(out_dtype)
+        codes_kn = b.view(torch.uint8).numpy()
+        packed = O.prepack_kn(codes_kn)
+        bias_np = bias.numpy() if out_dtype == torch.float16 else bias.view(torch.int16).numpy().view(np.uint16)
+        od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+        ref = O.scaled_mm_ref(a.numpy(), packed, np.float32(2.34), bias_np, od,
+                              "e5m2" if b_dtype == torch.float8_e5m2 else "e4m3")
+        bp = hk.prepack_b_for_scaled_mm(b.to(cuda))
+        assert np.array_equal(bp.view(torch.uint8).cpu().numpy(), packed)
+        s = torch.tensor(2.34, device=cuda)
+        for cfg in hk._CONFIGS:
+            bm, bn, ck = 16 * cfg[0] * cfg[3], 16 * cfg[1] * cfg[4], 16 * cfg[2]
+            if M % bm or N % bn or K % ck:
+                continue
+            y = hk.scaled_mm_hip_configured(a.to(cuda), bp, s, bias.to(cuda), out_dtype, *cfg)
+            torch.cuda.synchronize()
+            assert_gemm_close(y, ref, out_dtype, f"{M}x{N}x{K} {cfg} {b_dtype}")
+
+
+def test_special_weights(cuda):
+    g = torch.Generator().manual_seed(2)
+    M, K, N = 192, 256, 128
+    a = torch.randn(M, K, generator=g).half()
+    ad = a.to(cuda)
+    ones_np = O.prepack_kn(np.full((K, N), 0x3C, np.uint8))
+    ones = to_dev_codes(ones_np, cuda)
+    for cfg in [(2, 4, 4, 8, 4), (1, 1, 2, 1, 2)]:
+        for m in (M, 16):
+            y = capi_scaled_mm(ad[:m].contiguous(), ones, None, None, torch.float16, cfg)
+            assert (y == y[:, :1]).all(), "all-ones weight: every column is the row sum"
+            ref = O.scaled_mm_ref(a.numpy()[:m], ones_np, None, None, O.DT_F16)
+            assert_gemm_close(y, ref, torch.float16, f"row sums {cfg} m={m}")
+    eye = np.zeros((K, K), np.uint8)
+    eye[np.arange(K), np.arange(K)] = 0x3C
+    y = capi_scaled_mm(ad, to_dev_codes(O.prepack_kn(eye), cuda), None, None, torch.float16)
+    assert torch.equal(y.cpu(), a)
+    # scale only, no bias; bias only, no scale
+    packed, s = weight_like(N, K, g)
+    bd = to_dev_codes(packed, cuda)
+    ref = O.scaled_mm_ref(a.numpy(), packed, s, None, O.DT_F16)
+    assert_gemm_close(capi_scaled_mm(ad, bd, torch.tensor([s], device=cuda), None, torch.float16), ref,
+                      torch.float16)
+    bias = (torch.randn(N, generator=g)).half()
+    ref = O.scaled_mm_ref(a.numpy(), packed, None, bias.numpy(), O.DT_F16)
+    assert_gemm_close(capi_scaled_mm(ad, bd, None, bias.to(cuda), torch.float16), ref, torch.float16)
+
+
+def test_inf_nan_propagation(cuda):
+    M, K, N = 64, 128, 64
+    a = torch.ones(M, K, dtype=torch.float16)
+    a[3, 5] = float("inf")
+    a[7, 9] = float("nan")
+    codes = np.full((K, N), 0x3C, np.uint8)
+    codes[5, 10] = 0xBC  # -1 meets +inf -> -inf in column 10
+    ref = O.scaled_mm_ref(a.numpy(), O.prepack_kn(codes), None, None, O.DT_F16)
+    for cfg in [(2, 4, 4, 8, 4), (1, 1, 2, 1, 2)]:
+        y = capi_scaled_mm(a.to(cuda), to_dev_codes(O.prepack_kn(codes), cuda), None, None, torch.float16, cfg)
+        assert_gemm_close(y, ref, torch.float16, "inf/nan")
+    for m in (80, 16):  # overflow to inf in the fp16 output
+        big = torch.full((m, K), 60000.0, dtype=torch.float16)
+        y = capi_scaled_mm(big.to(cuda), to_dev_codes(O.prepack_kn(np.full((K, N), 0x3C, np.uint8)), cuda),
+                           None, None, torch.float16)
+        assert torch.isinf(y).all()
+
+
+def test_deterministic(cuda):
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(512, 1024, generator=g).half().to(cuda)
+    packed, s = weight_like(768, 1024, g)
+    bd = to_dev_codes(packed, cuda)
+    sd = torch.tensor([s], device=cuda)
+    for cfg in [(2, 4, 4, 8, 4), (1, 1, 2, 1, 2)]:
+        y1 = capi_scaled_mm(a, bd, sd, None, torch.float16, cfg)
+        y2 = capi_scaled_mm(a, bd, sd, None, torch.float16, cfg)
+        assert torch.equal(y1, y2)
+    # every tile kernel sums K in the same order: bit-identical across tiles
+    ys = [capi_scaled_mm(a, bd, sd, None, torch.float16, c) for c in TILE_CFGS]
+    for y in ys[1:]:
+        assert torch.equal(ys[0], y)
+
+
+def _sampled_rows_check(cuda, M, N, K, out_dtype, cfg, nrows=24, seed=0):
+    """Full-size run; the oracle recomputes a random subset of output rows."""
+    g = torch.Generator().manual_seed(seed)
+    packed, s = weight_like(N, K, g)
+    bias, bias_np = _bias_for(out_dtype, N, g)
+    gd = torch.Generator(device=cuda).manual_seed(seed)
+    a = torch.randn(M, K, generator=gd, device=cuda).half()
+    y = capi_scaled_mm(a, to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), bias.to(cuda),
+                       out_dtype, cfg)
+    rows = np.sort(np.random.default_rng(seed).choice(M, size=min(nrows, M), replace=False))
+    od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+    ref = O.scaled_mm_ref(a[torch.from_numpy(rows).to(cuda)].cpu().numpy(), packed, s, bias_np, od)
+    assert_gemm_close(y[torch.from_numpy(rows).to(cuda)], ref, out_dtype, f"{M}x{N}x{K}")
+    assert torch.isfinite(y).all()
+
+
+def test_baseline_config2_small_m(cuda):
+    _sampled_rows_check(cuda, 16, 4096, 4096, torch.float16, (1, 1, 2, 1, 2), nrows=16)
+
+
+@pytest.mark.parametrize("K,N", [(3072, 12288), (12288, 3072), (3072, 3072)])
+def test_baseline_config3_image_dit(cuda, K, N):
+    _sampled_rows_check(cuda, 4096, N, K, torch.bfloat16, (2, 4, 4, 8, 4))
+
+
+@pytest.mark.parametrize("K,N", [(5120, 13824), (13824, 5120), (5120, 5120)])
+def test_baseline_config4_video_dit(cuda, K, N):
+    _sampled_rows_check(cuda, 32768, N, K, torch.float16, (2, 4, 4, 8, 4), nrows=16)

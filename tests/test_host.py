@@ -1,0 +1,142 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every
+declared symbol, argument validation fails the way the reference's op does,
+and config/autotune helpers keep the reference's semantics. No kernel runs."""
+
+import re
+
+import pytest
+import torch
+
+from conftest import REPO
+
+
+def _declared_functions():
+    text = (REPO / "include" / "featherops_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*([a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    from featherops_amd.kernel.hip import _lib
+
+    L = _lib.lib()
+    names = _declared_functions()
+    assert "launch_scaled_mm" in names and len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header exactly"
+    assert L.feather_abi_version() == 1
+    assert L.feather_status_string(1) == b"invalid argument"
+
+
+def test_capi_rejects_without_launching(pkg):
+    from featherops_amd.kernel.hip import _lib
+
+    L = _lib.lib()
+    # unknown config tuple -> false before any HIP call (reference hip_kernel.cu:631)
+    assert not L.launch_scaled_mm(None, None, None, None, None, 256, 256, 256, 0, 0, 3, 3, 3, 3, 3, 1, 0, None)
+    # N not a multiple of 16
+    assert not L.launch_scaled_mm(None, None, None, None, None, 256, 250, 256, 0, 0, 1, 1, 2, 1, 2, 1, 0, None)
+    # bad dtypes
+    assert not L.launch_scaled_mm(None, None, None, None, None, 256, 256, 256, 0, 0, 1, 1, 2, 1, 2, 7, 0, None)
+    assert not L.launch_scaled_mm(None, None, None, None, None, 256, 256, 256, 0, 0, 1, 1, 2, 1, 2, 1, 5, None)
+    assert L.feather_prepack_transpose(None, None, 16, 16, None) == 1
+    assert L.feather_quantize_prepack_e5m2(None, 0, 16, 16, None, 0, None, None, None, None) == 1
+    assert L.feather_bf16_to_fp16(None, None, -1, None) == 1
+    assert L.feather_bf16_to_fp16(None, None, 0, None) == 0
+    assert L.feather_dequantize_e5m2(None, None, None, 0, 16, 16, None) == 1
+
+
+def test_kernel_id_mapping(hk):
+    assert hk.kernel_id(32768, 13824, 5120, (2, 4, 4, 8, 4)) == 1  # 256x256 tile
+    assert hk.kernel_id(16, 4096, 4096, (1, 1, 2, 1, 2)) == 10  # small-M
+    assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 3  # BlockM 128, BlockN 256
+    assert hk.kernel_id(4096, 4096, 4096, (3, 3, 3, 3, 3)) == 0
+    for cfg in hk._CONFIGS:
+        assert hk.kernel_id(1024, 1024, 1024, cfg) in (1, 2, 3, 4, 5, 6)
+
+
+def test_configs_keep_reference_entries(hk):
+    ref = {(1, 1, 2, 1, 2), (1, 1, 4, 1, 2), (1, 2, 2, 1, 2), (1, 2, 4, 1, 2), (1, 4, 2, 1, 2), (1, 4, 4, 1, 2),
+           (1, 8, 2, 1, 2), (1, 8, 4, 1, 2), (1, 1, 2, 2, 2), (1, 1, 4, 2, 2), (1, 1, 2, 4, 4), (1, 1, 4, 4, 4),
+           (1, 2, 2, 2, 2), (1, 2, 4, 2, 2), (2, 1, 2, 2, 2), (2, 1, 4, 2, 2), (1, 4, 2, 4, 2), (1, 4, 4, 4, 2),
+           (1, 8, 2, 8, 2), (1, 8, 4, 8, 2), (2, 2, 2, 4, 4), (2, 2, 4, 4, 4), (2, 4, 2, 4, 2), (2, 4, 4, 4, 2),
+           (2, 4, 2, 4, 4), (2, 4, 4, 4, 4), (4, 2, 2, 2, 4), (4, 2, 4, 2, 4)}
+    assert ref <= set(hk._CONFIGS)
+    assert hk._CONFIGS == sorted(hk._CONFIGS, key=lambda x: (x[0], x[1], x[3], x[4], x[2]))
+
+
+def test_config_compatible_rules(pkg):
+    from featherops_amd.kernel.hip import utils
+
+    assert utils._config_compatible((1, 1, 2, 1, 2), 16, 128, 128)
+    assert not utils._config_compatible((1, 1, 2, 2, 2), 16, 128, 128)  # BlockM 32
+    assert not utils._config_compatible((1, 1, 4, 1, 2), 16, 128, 96)  # ChunkK 64
+    # large shapes need blocks >= 64 (utils.py:141-142)
+    assert not utils._config_compatible((1, 1, 2, 1, 2), 4096, 4096, 4096)
+    assert utils._config_compatible((2, 4, 4, 8, 4), 32768, 13824, 5120)
+    a = torch.empty(16, 128, dtype=torch.float16)
+    b = torch.empty(8, 128, 16, dtype=torch.uint8)
+    assert utils.get_compatible_config(a, b, 1, [(1, 1, 2, 2, 2), (1, 1, 2, 1, 2)]) == (1, 1, 2, 1, 2)
+    with pytest.raises(RuntimeError, match="No compatible config"):
+        utils.get_compatible_config(a, b, 1, [(1, 1, 2, 2, 2)])
+
+
+def _good_args(M=64, N=128, K=256, out=torch.float16):
+    a = torch.empty(M, K, dtype=torch.float16)
+    b = torch.empty(K // 16, N, 16, dtype=torch.float8_e5m2)
+    c = torch.empty(M, N, dtype=out)
+    return a, b, torch.ones((), dtype=torch.float32), torch.zeros(N, dtype=out), c
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: dict(a=a["a"].float()), "a must be float16"),
+    (lambda a: dict(c=a["c"].float()), "c must be float16 or bfloat16"),
+    (lambda a: dict(b=a["b"].view(torch.uint8)), "b_prepacked must be float8_e5m2"),
+    (lambda a: dict(b_dtype=2), "b_dtype must be 0"),
+    (lambda a: dict(a=a["a"][:, :128]), r"b_prepacked.shape\[0\] must equal K/16"),
+    (lambda a: dict(a=torch.empty(64, 264, dtype=torch.float16)), "K must be divisible by 16"),
+    (lambda a: dict(c=torch.empty(32, 128, dtype=torch.float16)), r"c.shape\[0\] must equal M"),
+    (lambda a: dict(a=torch.empty(256, 64, dtype=torch.float16).t()), r"a.stride\(0\) must equal K"),
+    (lambda a: dict(scale=torch.ones(2)), "scale must have one element"),
+    (lambda a: dict(scale=torch.ones((), dtype=torch.float16)), "scale must be float32"),
+    (lambda a: dict(bias=torch.zeros(128, dtype=torch.bfloat16)), "bias must have the same dtype as c"),
+    (lambda a: dict(bias=torch.zeros(64, dtype=torch.float16)), "bias must have N elements"),
+    (lambda a: dict(cfg=(1, 1, 2, 8, 2)), r"M \(64\) must be divisible by kBlockM \(128\)"),
+    (lambda a: dict(cfg=(1, 8, 4, 1, 2)), r"N \(128\) must be divisible by kBlockN \(256\)"),
+])
+def test_validation_messages(hk, mutate, msg):
+    a, b, s, bias, c = _good_args()
+    args = dict(a=a, b=b, scale=s, bias=bias, c=c, cfg=(1, 1, 2, 1, 2), b_dtype=1)
+    hk.validate_scaled_mm(args["a"], args["b"], args["scale"], args["bias"], args["c"], *args["cfg"],
+                          args["b_dtype"], require_cuda=False)
+    args.update(mutate(args))
+    with pytest.raises(RuntimeError, match=msg):
+        hk.validate_scaled_mm(args["a"], args["b"], args["scale"], args["bias"], args["c"], *args["cfg"],
+                              args["b_dtype"], require_cuda=False)
+
+
+def test_cpu_tensors_raise_loudly(hk):
+    a, b, s, bias, c = _good_args()
+    # the op has only a GPU kernel: CPU tensors hit torch's "no kernel for backend" error
+    with pytest.raises((RuntimeError, NotImplementedError), match="CUDA"):
+        torch.ops.feather_ops.scaled_mm.default(a, b, s, bias, c, 1, 1, 2, 1, 2, 1)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        hk._scaled_mm_native(a, b, s, bias, c, 1, 1, 2, 1, 2, 1)
+
+
+def test_fake_impl_shapes_for_compile(hk):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        a = torch.empty(64, 256, dtype=torch.float16)
+        b = torch.empty(16, 128, 16, dtype=torch.float8_e5m2)
+        out = hk._configured_op(a, b, None, None, torch.bfloat16, 1, 1, 2, 1, 2)
+        assert out.shape == (64, 128) and out.dtype == torch.bfloat16
+
+
+def test_ops_m_padding_rule(pkg):
+    from featherops_amd.comfy_feather import ops
+
+    assert [ops._m_block(m) for m in (1, 64, 65, 128, 129, 256, 257)] == [16, 16, 32, 32, 64, 64, 128]

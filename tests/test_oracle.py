@@ -1,0 +1,225 @@
+"""CPU checks that pin the numpy oracle (oracle/feather_oracle.py).
+
+Ground truths: torch's own fp8/bf16/fp16 casts (the reference's arithmetic is
+those casts), the reference's e5m2 known-answer table, closed forms and brute
+force on tiny shapes. The golden fixtures are checked to still equal the
+oracle."""
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import feather_oracle as O
+
+from conftest import GOLDEN
+
+ALL16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+def test_e5m2_decode_exhaustive_vs_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes).view(torch.float8_e5m2).to(torch.float32).numpy()
+    o = O.e5m2_decode(codes)
+    assert np.array_equal(np.isnan(t), np.isnan(o))
+    assert np.array_equal(t[~np.isnan(t)], o[~np.isnan(o)])
+
+
+def test_e5m2_known_answers():
+    # cpp_benchmarks/benchmark_scaled_mm_hip.cpp:127-137 of the reference
+    kat = {0xBC: -1.0, 0xBA: -0.75, 0xB8: -0.5, 0xB4: -0.25, 0x00: 0.0, 0x34: 0.25, 0x38: 0.5, 0x3A: 0.75, 0x3C: 1.0}
+    for code, val in kat.items():
+        assert O.e5m2_decode(np.array([code], np.uint8))[0] == val
+        assert O.e5m2_encode(np.array([val], np.float32))[0] == (0x80 if code == 0x00 and val < 0 else code)
+    # fp16 bits are the code shifted into the high byte for every code (the kernel's widen)
+    codes = np.arange(256, dtype=np.uint16)
+    widened = (codes << 8).astype(np.uint16).view(np.float16).astype(np.float32)
+    o = O.e5m2_decode(codes.astype(np.uint8))
+    assert np.array_equal(np.isnan(widened), np.isnan(o))
+    assert np.array_equal(widened[~np.isnan(o)], o[~np.isnan(o)])
+
+
+def test_e5m2_encode_exhaustive_fp16_bf16_vs_torch():
+    f16 = ALL16.view(np.float16)
+    t = torch.from_numpy(f16.copy()).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(O.e5m2_encode(f16.astype(np.float32)), t)
+    tb = torch.from_numpy(ALL16.view(np.int16).copy()).view(torch.bfloat16).to(torch.float8_e5m2)
+    assert np.array_equal(O.e5m2_encode(O.bf16_bits_to_f32(ALL16)), tb.view(torch.uint8).numpy())
+
+
+def test_e5m2_encode_fp32_boundaries_vs_torch():
+    # every code value and every midpoint, +-64 ulps around each, both signs
+    vals = O.E5M2_TABLE[np.isfinite(O.E5M2_TABLE)]
+    vals = np.unique(np.abs(vals))
+    mids = (vals[1:] + vals[:-1]) / 2
+    pts = np.concatenate([vals, mids, [61440.0, 65536.0, 2.0**-17, 2.0**-16 * 1.5]]).astype(np.float32)
+    bits = pts.view(np.uint32)[:, None].astype(np.int64) + np.arange(-64, 65)[None, :]
+    bits = np.clip(bits, 0, 0x7FFFFFFF).astype(np.uint32).reshape(-1)
+    x = np.concatenate([bits.view(np.float32), -bits.view(np.float32)])
+    rng = np.random.default_rng(0)
+    x = np.concatenate([x, rng.integers(0, 2**32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    t = torch.from_numpy(x.copy()).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(O.e5m2_encode(x), t)
+
+
+def test_bf16_and_fp16_rounding_vs_torch():
+    rng = np.random.default_rng(1)
+    x = rng.integers(0, 2**32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    # include exact ties for bf16
+    ties = (rng.integers(0, 2**16, 4096, dtype=np.uint64).astype(np.uint32) << 16 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties, np.array([3.4028235e38, -3.4028235e38, 0.0, -0.0], np.float32)])
+    tb = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ob = O.f32_to_bf16_rne(x)
+    nan = np.isnan(x)
+    assert np.array_equal(ob[~nan], tb[~nan])
+    assert np.all(ob[nan] == 0x7FC0)
+    th = torch.from_numpy(x.copy()).to(torch.float16).numpy()
+    oh = O.f32_to_fp16_rne(x)
+    assert np.array_equal(oh[~nan].view(np.uint16), th[~nan].view(np.uint16))
+
+
+def test_bf16_to_fp16_rtz_closed_form():
+    out = O.bf16_to_fp16_rtz(ALL16)
+    v = O.bf16_bits_to_f32(ALL16).astype(np.float64)
+    o = out.view(np.float16).astype(np.float64)
+    fin = np.isfinite(v)
+    normal = fin & (np.abs(v) >= 2.0**-14) & (np.abs(v) <= 65504)
+    # every bf16 value in fp16's normal range is exact in fp16: RTZ == RNE == torch
+    t = torch.from_numpy(ALL16.view(np.int16).copy()).view(torch.bfloat16).to(torch.float16).numpy()
+    assert np.array_equal(out[normal], t[normal].view(np.uint16))
+    # saturation instead of inf
+    big = fin & (np.abs(v) > 65504)
+    assert np.all(np.abs(o[big]) == 65504) and np.array_equal(np.sign(o[big]), np.sign(v[big]))
+    # subnormal range: truncation, |o| <= |v| < |o| + 2^-24, same sign
+    small = fin & (np.abs(v) < 2.0**-14)
+    assert np.all(np.abs(o[small]) <= np.abs(v[small]))
+    assert np.all(np.abs(v[small]) - np.abs(o[small]) < 2.0**-24)
+    assert np.array_equal(np.signbit(o[small]), np.signbit(v[small]))
+    assert np.all(np.isinf(o[np.isinf(v)])) and np.all(np.isnan(o[np.isnan(v)]))
+
+
+@pytest.mark.parametrize("n,k", [(1, 16), (3, 32), (5, 48), (64, 64)])
+def test_prepack_index_identity(n, k):
+    w = np.random.default_rng(n).integers(0, 256, (n, k), dtype=np.uint8)
+    p = O.prepack_transpose(w)
+    for i in range(k // 16):
+        for r in range(n):
+            for j in range(16):
+                assert p[i, r, j] == w[r, 16 * i + j]
+    assert np.array_equal(O.unprepack_transpose(p), w)
+    b = w.T.copy()  # (K, N)
+    pb = O.prepack_kn(b)
+    assert np.array_equal(pb, p)  # (K,N) prepack of W^T == (N,K) prepack of W
+    assert np.array_equal(O.unprepack_kn(pb), b)
+
+
+def _torch_quant_steps(x: torch.Tensor, clamp_fp16: bool):
+    """quant.py:52-74 evaluated with torch CPU ops, one step per line."""
+    s = torch.amax(x.abs()).to(torch.float32) / 57344.0
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    if clamp_fp16:
+        s = 1.0 / torch.clamp(1.0 / s, min=-65504.0, max=65504.0)
+    inv = (1.0 / s).to(x.dtype)
+    return (x * inv).to(torch.float8_e5m2).view(torch.uint8).numpy(), np.float32(s.item())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("std", [0.02, 1.0, 300.0])
+def test_quantize_native_vs_torch_steps(dtype, std):
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(64, 128, generator=g) * std).to(dtype)
+    t_codes, t_s = _torch_quant_steps(x, dtype == torch.float16)
+    if dtype == torch.bfloat16:
+        xin, dt = x.view(torch.int16).numpy().view(np.uint16), O.DT_BF16
+    else:
+        xin, dt = x.numpy(), {torch.float16: O.DT_F16, torch.float32: O.DT_F32}[dtype]
+    codes, s = O.quantize_native(xin, dt)
+    assert s == t_s
+    assert np.array_equal(codes, t_codes)
+
+
+def test_quantize_load_invariants():
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(256, 512, generator=g) * 0.02).numpy()
+    codes, s = O.quantize_load(w, O.DT_F32)
+    amax = np.float32(np.abs(w).max())
+    assert s == np.float32(amax / np.float32(57344.0))
+    # the largest element lands exactly on the largest finite code
+    idx = np.unravel_index(np.argmax(np.abs(w)), w.shape)
+    assert codes[idx] & 0x7F == 0x7B
+    assert np.all((codes & 0x7F) <= 0x7B)  # nothing overflows
+    # dequantized values are within half a code step (relative 2^-3) of w
+    deq = O.e5m2_decode(codes).astype(np.float64) * s
+    big = np.abs(w) > 2.0**-14 * s
+    assert np.all(np.abs(deq[big] - w[big]) <= np.abs(w[big]) * 2.0**-3 + 1e-30)
+    # checkpoint scale multiplies first: quantizing w*2 with ckpt 1 == w with ckpt 2
+    c2, s2 = O.quantize_load(w, O.DT_F32, ckpt_scale=2.0)
+    c3, s3 = O.quantize_load((w * np.float32(2.0)).astype(np.float32), O.DT_F32)
+    assert np.array_equal(c2, c3) and s2 == s3
+
+
+def test_quantize_special_cases():
+    z = np.zeros((16, 32), np.float16)
+    codes, s = O.quantize_native(z, O.DT_F16)
+    assert s == 1.0 and np.all(codes == 0)
+    # fp16 clamp: amax < 57344/65504 gives scale 1/65504 rather than amax/57344
+    w = np.full((16, 32), 0.09, np.float16)
+    _, s16 = O.quantize_native(w, O.DT_F16)
+    assert s16 == np.float32(1.0) / np.float32(65504.0)
+    _, s32 = O.quantize_load(w, O.DT_F16)
+    assert s32 == np.float32(np.float32(np.float16(0.09)) / np.float32(57344.0))
+
+
+def test_scaled_mm_oracle_brute_force():
+    rng = np.random.default_rng(5)
+    M, N, K = 3, 16, 32
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    codes = rng.integers(0, 0x7C, (K, N), dtype=np.uint8) | (rng.integers(0, 2, (K, N), dtype=np.uint8) << 7)
+    bp = O.prepack_kn(codes)
+    s = np.float32(0.37)
+    exact = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            exact[m, n] = sum(float(a[m, k]) * float(O.E5M2_TABLE[codes[k, n]]) for k in range(K))
+    got = O.scaled_mm_ref_f32(a, bp, s)
+    assert np.allclose(got, exact * float(s), rtol=1e-12, atol=0)
+    y = O.scaled_mm_ref(a, bp, s, None, O.DT_F16)
+    assert np.array_equal(y, (np.float32(exact) * s).astype(np.float16))
+
+
+def test_scaled_mm_oracle_special_weights():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((8, 64)).astype(np.float16)
+    ones = np.full((64, 16), 0x3C, np.uint8)  # 1.0
+    y = O.scaled_mm_ref_f32(a, O.prepack_kn(ones), None)
+    assert np.allclose(y, a.astype(np.float64).sum(1, keepdims=True).repeat(16, 1))
+    eye = np.zeros((64, 64), np.uint8)
+    eye[np.arange(64), np.arange(64)] = 0x3C
+    y = O.scaled_mm_ref(a, O.prepack_kn(eye), None, None, O.DT_F16)
+    assert np.array_equal(y, a)
+    # naive (fp16 product then scale) equals the fp32 path when nothing overflows and scale is a power of 2
+    b = rng.integers(0x30, 0x3C, (64, 16), dtype=np.uint8)
+    yn = O.scaled_mm_naive(a, O.prepack_kn(b), np.float32(0.5), None, O.DT_F16)
+    yr = O.scaled_mm_ref(a, O.prepack_kn(b), np.float32(0.5), None, O.DT_F16)
+    assert np.array_equal(yn, yr)
+
+
+def test_golden_fixtures_match_oracle():
+    z = np.load(GOLDEN / "e5m2_codes.npz")
+    assert np.array_equal(z["from_fp16"], O.e5m2_encode(ALL16.view(np.float16).astype(np.float32)))
+    r = np.load(GOLDEN / "bf16_rtz.npz")
+    assert np.array_equal(r["fp16_bits"], O.bf16_to_fp16_rtz(ALL16))
+    q = np.load(GOLDEN / "quant_c1.npz")
+    g = torch.Generator().manual_seed(0)
+    w32 = torch.randn(1024, 1024, generator=g) * 0.02
+    codes, s = O.quantize_load(w32.half().numpy(), O.DT_F16)
+    assert s == q["load_f16_scale"][0]
+    packed = O.prepack_transpose(codes)
+    assert hashlib.sha256(packed.tobytes()).digest() == q["load_f16_sha256"].tobytes()
+    assert np.array_equal(codes[q["rows"]], q["load_f16_rows"])
+    # the patch path on fp16 hits the reciprocal clamp (amax ~0.1 < 0.875)
+    assert q["native_f16_scale"][0] == np.float32(1.0) / np.float32(65504.0)
+    gm = np.load(GOLDEN / "gemm_small.npz")
+    y = O.scaled_mm_ref(gm["a"], gm["b_prepacked"], gm["scale"][0], gm["bias_f16"], O.DT_F16)
+    assert np.array_equal(y, gm["out_f16"])
