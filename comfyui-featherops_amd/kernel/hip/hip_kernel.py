@@ -195,13 +195,20 @@ def _(a, b_prepacked, scale, bias, out_dtype, has_scale, has_bias, block_warps_m
     return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
 
 
-try:
+def _torch_at_least(major: int, minor: int) -> bool:
+    parts = torch.__version__.split("+")[0].split(".")
+    return (int(parts[0]), int(parts[1])) >= (major, minor)
+
+
+# Inductor's custom-op autotuning (the reference needs torch >= 2.12 for it,
+# README.md:46). Older inductors cannot bind this op's dtype argument during
+# autotuning, so there torch.compile runs the first compatible config.
+AUTOTUNE_UNDER_COMPILE = _torch_at_least(2, 12)
+if AUTOTUNE_UNDER_COMPILE:
     from torch._inductor.kernel.custom_op import register_custom_op_autotuning
 
     register_custom_op_autotuning(
         _autotuned_op, config_generator=lambda fake_tensors: generate_autotune_configs(fake_tensors, _CONFIGS, 1))
-except ImportError:  # inductor without custom-op autotuning: compile still uses the default config
-    pass
 
 
 def scaled_mm_hip(

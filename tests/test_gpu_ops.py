@@ -53,10 +53,10 @@ def test_feather_linear_excluded_and_patch(cuda, pkg):
     ops_cls = ops.feather_ops(out_dtype=torch.float16, excluded_names=("proj_out",))
     lin = ops_cls.Linear(64, 32)
     w = torch.randn(32, 64) * 0.1
-    lin._load_from_state_dict({"weight": w.clone()}, "proj_out.", {}, True, [], [], [])
+    lin._load_from_state_dict({"proj_out.weight": w.clone()}, "proj_out.", {}, True, [], [], [])
     assert not lin.is_quantized
     lin2 = ops_cls.Linear(64, 32)
-    lin2._load_from_state_dict({"weight": w.clone().to(cuda)}, "blocks.0.", {}, True, [], [], [])
+    lin2._load_from_state_dict({"blocks.0.weight": w.clone().to(cuda)}, "blocks.0.", {}, True, [], [], [])
     assert lin2.is_quantized
     deq = lin2.convert_weight(lin2.weight)
     assert deq.shape == (32, 64) and deq.dtype == torch.float16
