@@ -16,14 +16,14 @@ struct Cfg {
 };
 
 // Reference configurations (kernel/hip/hip_kernel.py:60-89, hip_kernel.cu:603-630)
-// followed by two gfx950 tiles the reference has no tuple for.
+// followed by three gfx950 tiles the reference has no tuple for.
 constexpr Cfg kConfigs[] = {
     {1, 1, 2, 1, 2}, {1, 1, 4, 1, 2}, {1, 2, 2, 1, 2}, {1, 2, 4, 1, 2}, {1, 4, 2, 1, 2}, {1, 4, 4, 1, 2},
     {1, 8, 2, 1, 2}, {1, 8, 4, 1, 2}, {1, 1, 2, 2, 2}, {1, 1, 4, 2, 2}, {1, 1, 2, 4, 4}, {1, 1, 4, 4, 4},
     {1, 2, 2, 2, 2}, {1, 2, 4, 2, 2}, {2, 1, 2, 2, 2}, {2, 1, 4, 2, 2}, {1, 4, 2, 4, 2}, {1, 4, 4, 4, 2},
     {1, 8, 2, 8, 2}, {1, 8, 4, 8, 2}, {2, 2, 2, 4, 4}, {2, 2, 4, 4, 4}, {2, 4, 2, 4, 2}, {2, 4, 4, 4, 2},
     {2, 4, 2, 4, 4}, {2, 4, 4, 4, 4}, {4, 2, 2, 2, 4}, {4, 2, 4, 2, 4},
-    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4},
+    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4}, {4, 2, 4, 4, 8},
 };
 
 bool known_config(int wm, int wn, int u, int rm, int rn) {
@@ -32,14 +32,20 @@ bool known_config(int wm, int wn, int u, int rm, int rn) {
     return false;
 }
 
-int kernel_for(int64_t M, int wm, int wn, int rm, int rn) {
+// The tuple picks the output tile (BlockM x BlockN, capped at 256); the
+// LDS-DMA pipeline serves K % 64 == 0, the register-staged tile the rest.
+int kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     if (M <= 64) return feather::kSmallM;
     const int bm = 16 * wm * rm;
     const int bn = 16 * wn * rn;
-    if (bm >= 256 && bn >= 256) return feather::kTile256x256;
-    if (bm >= 256) return feather::kTile256x128;
-    if (bn >= 256) return bm >= 128 ? feather::kTile128x256 : feather::kTile64x128;
-    if (bm >= 128 && bn >= 128) return feather::kTile128x128;
+    const bool lds = K % 64 == 0;
+    if (bm >= 256 && bn >= 256) {
+        if (!lds) return feather::kTile256x256;
+        return wm > wn ? feather::kLds256x256w4x2 : feather::kLds256x256w2x4;
+    }
+    if (bm >= 256) return lds ? feather::kLds256x128 : feather::kTile256x128;
+    if (bn >= 256) return bm >= 128 ? (lds ? feather::kLds128x256 : feather::kTile128x256) : feather::kTile64x128;
+    if (bm >= 128 && bn >= 128) return lds ? feather::kLds128x128 : feather::kTile128x128;
     if (bn >= 128) return feather::kTile64x128;
     return feather::kTile64x64;
 }
@@ -60,7 +66,7 @@ int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps
                                 int repeat_m, int repeat_n) {
     if (!known_config(block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n)) return feather::kKernelNone;
     if (!sizes_ok(M, N, K)) return feather::kKernelNone;
-    return kernel_for(M, block_warps_m, block_warps_n, repeat_m, repeat_n);
+    return kernel_for(M, K, block_warps_m, block_warps_n, repeat_m, repeat_n);
 }
 
 bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,
@@ -87,6 +93,7 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
     p.group_m = 0;
     if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, stream);
+    if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
 }
 

@@ -31,9 +31,16 @@ enum KernelId : int {
     kTile64x128 = 5,
     kTile64x64 = 6,
     kSmallM = 10,  // M <= 64: split-K inside the workgroup, one 16-column strip per workgroup
+    // LDS-DMA pipelined tiles (K % 64 == 0)
+    kLds256x256w2x4 = 20,
+    kLds256x256w4x2 = 21,
+    kLds256x128 = 22,
+    kLds128x256 = 23,
+    kLds128x128 = 24,
 };
 
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
 bool launch_smallm_kernel(const MmArgs& p, hipStream_t stream);
+bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
 
 }  // namespace feather

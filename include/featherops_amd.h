@@ -46,7 +46,7 @@ extern "C" {
  *   has_scale / has_bias: 0 or 1; scale / bias are only read when set.
  *   (block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n): one of the
  *   configurations the reference lists (hip_kernel.py:60-89) or one of the
- *   gfx950 additions (2,4,4,8,4), (4,2,4,4,4). The tuple keeps the reference's
+ *   gfx950 additions (2,4,4,8,4), (4,2,4,4,8), (4,2,4,4,4). The tuple keeps the reference's
  *   divisibility meaning (BlockM = 16*wm*rm, BlockN = 16*wn*rn, ChunkK = 16*u)
  *   for callers that pad to it; the kernels themselves accept any M.
  *   b_dtype: FEATHER_B_E4M3FN or FEATHER_B_E5M2. output_dtype: 0 fp16, 1 bf16.

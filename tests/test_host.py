@@ -48,13 +48,16 @@ def test_capi_rejects_without_launching(pkg):
 
 
 def test_kernel_id_mapping(hk):
-    assert hk.kernel_id(32768, 13824, 5120, (2, 4, 4, 8, 4)) == 1  # 256x256 tile
+    assert hk.kernel_id(32768, 13824, 5120, (2, 4, 4, 8, 4)) == 20  # 256x256 LDS-DMA pipeline, 2x4 waves
+    assert hk.kernel_id(32768, 13824, 5120, (4, 2, 4, 4, 8)) == 21  # same tile, 4x2 waves
+    assert hk.kernel_id(32768, 13824, 5136, (2, 4, 4, 8, 4)) == 1  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(16, 4096, 4096, (1, 1, 2, 1, 2)) == 10  # small-M
     assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 10
-    assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 3  # BlockM 128, BlockN 256
+    assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 23  # BlockM 128, BlockN 256
     assert hk.kernel_id(4096, 4096, 4096, (3, 3, 3, 3, 3)) == 0
+    assert hk.kernel_id(4096, 4096, 4090, (2, 4, 4, 8, 4)) == 0  # K % 16 != 0
     for cfg in hk._CONFIGS:
-        assert hk.kernel_id(1024, 1024, 1024, cfg) in (1, 2, 3, 4, 5, 6)
+        assert hk.kernel_id(1024, 1024, 1024, cfg) in (5, 6, 20, 21, 22, 23, 24)
 
 
 def test_configs_keep_reference_entries(hk):
