@@ -2,6 +2,7 @@
 // include/featherops_amd.h). Validation that needs only sizes and pointers
 // lives here; dtype/stride checks of torch tensors live in the Python layer.
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "featherops_amd.h"
 #include "quant_prepack.h"
@@ -56,6 +57,16 @@ bool sizes_ok(int64_t M, int64_t N, int64_t K) {
            (K / 16) * N <= lim;
 }
 
+// FEATHEROPS_GROUP_M: tile-raster group height of the tile kernels (tuning knob, default 4).
+int tuning_group_m() {
+    static const int g = [] {
+        const char* e = getenv("FEATHEROPS_GROUP_M");
+        const int v = e ? atoi(e) : 4;
+        return v > 0 ? v : 4;
+    }();
+    return g;
+}
+
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
 }  // namespace
@@ -91,7 +102,7 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
     p.has_bias = has_bias ? 1 : 0;
     p.out_bf16 = output_dtype == 1;
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
-    p.group_m = 0;
+    p.group_m = tuning_group_m();
     if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, stream);
     if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);

@@ -7,15 +7,23 @@
 // Differences from the register-staged tile kernel:
 //   * global -> LDS copies use gfx950's global_load_lds_dwordx4: each wave
 //     instruction moves 64 x 16 bytes straight into a contiguous 1 KB of LDS,
-//     with no VGPR staging and no ds_write. The A swizzle (chunk c of row r at
-//     c ^ (r & 7)) is applied on the global side: the lane that fills LDS chunk
-//     p of row r fetches logical chunk p ^ (r & 7);
-//   * three LDS stage buffers; loads for stage kt + 2 are issued right after
-//     the barrier of stage kt, so every copy has two stages of MFMA work to
-//     land. One barrier per stage, preceded by an explicit vmcnt wait that
-//     leaves the younger stage in flight;
+//     with no VGPR staging and no ds_write. Addresses are a wave-uniform SGPR
+//     base (advanced per stage with scalar adds) plus a fixed 32-bit per-lane
+//     offset;
+//   * A rows are 128 bytes in LDS; chunk c of row r is stored at c ^ swz(r).
+//     The swizzle is applied on the global side: the lane that fills LDS chunk
+//     p of row r fetches logical chunk p ^ swz(r);
+//   * three LDS stage buffers; the copies for stage kt + 2 are issued right
+//     after the barrier that publishes stage kt, so every copy has two stages
+//     of MFMA work to land. The barrier is preceded by an explicit vmcnt wait
+//     that leaves the younger stage's copies in flight;
+//   * per stage, the K halves are processed one after the other (all M
+//     repeats of K half 0, then of K half 1), so only half of the widened B
+//     operands are live at a time;
 //   * rows past M / columns past N are clamped to the last valid row/column
-//     (their results are computed and dropped), so every lane loads in bounds.
+//     (their results are computed and dropped), so every copy is in bounds.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "feather_common.h"
@@ -33,6 +41,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// vmcnt(N) and lgkmcnt(0) in one s_waitcnt.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
 // Workgroup barrier that neither waits for outstanding LDS-DMA copies (the
 // caller waits for exactly the ones it needs) nor lets the compiler move
 // memory accesses across it.
@@ -40,28 +55,34 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 16 bytes per lane from gsrc into LDS at lds_dst + 16 * lane (lds_dst is
-// wave-uniform). Written as inline asm so that the compiler's wait-count
-// tracking does not treat the copy as an LDS write that every later ds_read
-// might alias (it would put a vmcnt(0) in front of the current stage's reads,
-// draining the copies of the next stages); the kernel waits with explicit
-// vmcnt counts instead. M0 is saved and restored around the copy.
-__device__ __forceinline__ void dma16(const void* gsrc, uint8_t* lds_dst) {
+// A rows are 128 bytes (8 chunks of 16 B). A ds_read_b128 of 16 rows (lanes
+// 0-15, same logical chunk) is served 256 bytes (64 banks) per cycle: rows r
+// and r + 1 share a 256-byte bank row, so rows of equal parity get distinct
+// chunks.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+// 16 bytes per lane from sbase + voff into LDS at lds_dst + 16 * lane
+// (sbase and lds_dst wave-uniform). Inline asm so that the compiler's
+// wait-count tracking does not treat the copy as an LDS write that every later
+// ds_read might alias (it would put a vmcnt(0) in front of the current stage's
+// reads, draining the copies of the next stages); the kernel waits with
+// explicit vmcnt counts instead. M0 is saved and restored around the copy.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint8_t* lds_dst) {
     const uint32_t lds_off =
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds_dst)));
     uint32_t saved_m0;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b32 m0, %3\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved_m0)
-        : "v"(gsrc), "s"(lds_off)
+        : "v"(voff), "s"(sbase), "s"(lds_off)
         : "memory");
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool kBf16, bool kE4m3>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
@@ -85,10 +106,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     constexpr int kCRowBytes = WTN * 2 + 16;
     constexpr int kCWaveBytes = 16 * kCRowBytes;
     static_assert(kWaves * kCWaveBytes <= kStage, "epilogue staging reuses stage buffer 0");
-    static_assert(STAGES == 3, "the main loop is unrolled for three stage buffers");
-    // One LDS object per stage: the compiler can then tell that a ds_read of
-    // the current stage does not alias the LDS-DMA copies in flight into the
-    // other stages, and does not insert a vmcnt(0) wait in front of it.
+    // One LDS object per stage buffer (the main loop is unrolled by three).
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf2[kStage];
@@ -111,7 +129,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const int n0 = tn * BN;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int wave_m = wave % WAVES_M;
     const int wave_n = wave / WAVES_M;
@@ -119,29 +137,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const int lg = lane >> 4;
     const int nk = K / kBK;
 
-    // ---- per-lane global sources (stage 0); advanced by 64 K per stage ----
-    // A copy j of this wave fills rows r0..r0+7, r0 = (j * kWaves + wave) * 8.
-    const uint16_t* a_src[kAPerWave];
+    // ---- per-lane copy offsets (fixed), per-stage SGPR bases ----
+    // A copy j of this wave fills rows r0..r0+7 of the tile, r0 = (j * kWaves + wave) * 8.
+    uint32_t a_off[kAPerWave];
 #pragma unroll
     for (int j = 0; j < kAPerWave; ++j) {
         const int row = (j * kWaves + wave) * 8 + (lane >> 3);
-        const int p = lane & 7;
-        const int c = p ^ (row & 7);
-        int grow = m0 + row;
-        grow = grow < M ? grow : M - 1;
-        a_src[j] = A + static_cast<int64_t>(grow) * K + c * 8;
+        const int c = (lane & 7) ^ swz(row);
+        const int lrow = (m0 + row < M ? m0 + row : M - 1) - m0;
+        a_off[j] = static_cast<uint32_t>(lrow * K * 2 + c * 16);
     }
-    // B copy j of this wave covers chunks [base, base+64) of the (4 x BN) stage, base = (j*kWaves+wave)*64.
-    const uint8_t* b_src[kBPerWave];
+    // B copy j covers chunks [base, base+64) of the (4 x BN) stage, base = (j*kWaves+wave)*64.
+    uint32_t b_off[kBPerWave];
 #pragma unroll
     for (int j = 0; j < kBPerWave; ++j) {
         const int chunk = (j * kWaves + wave) * 64 + lane;
         const int kb = chunk / BN;
-        int gcol = n0 + chunk % BN;
-        gcol = gcol < N ? gcol : N - 1;
-        b_src[j] = Bp + (static_cast<int64_t>(kb) * N + gcol) * 16;
+        const int lcol = (n0 + chunk % BN < N ? n0 + chunk % BN : N - 1) - n0;
+        b_off[j] = static_cast<uint32_t>((kb * N + lcol) * 16);
     }
-    const int64_t b_stage_stride = static_cast<int64_t>(N) * 64;  // 4 K groups of N x 16 bytes
+    const uint8_t* a_base = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * K * 2;
+    const uint8_t* b_base = Bp + static_cast<int64_t>(n0) * 16;
+    const int64_t b_stage_bytes = static_cast<int64_t>(N) * 64;  // 4 K groups of N x 16 bytes
 
     auto stage_buf = [&](auto tag) -> uint8_t* {
         constexpr int b = decltype(tag)::value;
@@ -152,12 +169,23 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     auto issue_stage = [&](auto tag, int kt) {
         uint8_t* sa = stage_buf(tag);
         uint8_t* sb = sa + kAStage;
+        const uint8_t* ab = a_base + kt * (kBK * 2);
+        const uint8_t* bb = b_base + kt * b_stage_bytes;
 #pragma unroll
-        for (int j = 0; j < kAPerWave; ++j)
-            dma16(a_src[j] + kt * kBK, sa + ((j * kWaves + wave) * 8) * 128);
+        for (int j = 0; j < kAPerWave; ++j) dma16(ab, a_off[j], sa + ((j * kWaves + wave) * 8) * 128);
 #pragma unroll
-        for (int j = 0; j < kBPerWave; ++j)
-            dma16(b_src[j] + kt * b_stage_stride, sb + ((j * kWaves + wave) * 64) * 16);
+        for (int j = 0; j < kBPerWave; ++j) dma16(bb, b_off[j], sb + ((j * kWaves + wave) * 64) * 16);
+    };
+    // LDS byte offset of this lane's A operand for M repeat rm, K half kh
+    auto a_lds = [&](int rm, int kh) -> int {
+        const int row = wave_m * WTM + rm * 16 + lr;
+        return row * 128 + (((2 * lg + kh) ^ swz(row)) << 4);
+    };
+    auto read_b = [&](auto cur, uint4 (&braw)[RN]) {
+        const uint8_t* sb = stage_buf(cur) + kAStage;
+#pragma unroll
+        for (int rn = 0; rn < RN; ++rn)
+            braw[rn] = *reinterpret_cast<const uint4*>(sb + (lg * BN + wave_n * WTN + rn * 16 + lr) * 16);
     };
 
     f32x4 acc[RM][RN];
@@ -170,45 +198,81 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
 
-    // stage kt lives in buffer kt % 3; its copies were issued two stages earlier
-    auto run_stage = [&](auto cur, int kt) {
-        constexpr int c = decltype(cur)::value;
-        using Next = std::integral_constant<int, (c + 2) % 3>;
-        // copies of stage kt are done once at most the next stage's remain in flight
-        if (kt + 1 < nk) wait_vmcnt<kLoadsPerStage>();
-        else wait_vmcnt<0>();
-        stage_barrier();
-        if (kt + 2 < nk) issue_stage(Next{}, kt + 2);
-
+    // One K half of one stage: widen this half of the B operands, then run
+    // every M repeat. `hook(rm)` runs before the MFMAs of repeat rm.
+    auto half_stage = [&](auto cur, int kh, const uint4 (&braw)[RN], auto hook) {
         const uint8_t* sa = stage_buf(cur);
-        const uint8_t* sb = sa + kAStage;
-        half8_t bq[RN][2];
+        half8_t bq[RN];
 #pragma unroll
-        for (int rn = 0; rn < RN; ++rn) {
-            const int col = wave_n * WTN + rn * 16 + lr;
-            const uint4 raw = *reinterpret_cast<const uint4*>(sb + (lg * BN + col) * 16);
-            bq[rn][0] = widen_fp8x8<kE4m3>(raw.x, raw.y);
-            bq[rn][1] = widen_fp8x8<kE4m3>(raw.z, raw.w);
-        }
+        for (int rn = 0; rn < RN; ++rn)
+            bq[rn] = kh == 0 ? widen_fp8x8<kE4m3>(braw[rn].x, braw[rn].y) : widen_fp8x8<kE4m3>(braw[rn].z, braw[rn].w);
 #pragma unroll
         for (int rm = 0; rm < RM; ++rm) {
-            const int row = wave_m * WTM + rm * 16 + lr;
-            const uint8_t* rp = sa + row * 128;
-            const half8_t a0 = as_half8(*reinterpret_cast<const uint4*>(rp + (((2 * lg) ^ (row & 7)) << 4)));
-            const half8_t a1 = as_half8(*reinterpret_cast<const uint4*>(rp + (((2 * lg + 1) ^ (row & 7)) << 4)));
+            const half8_t a = as_half8(*reinterpret_cast<const uint4*>(sa + a_lds(rm, kh)));
+            hook(rm);
 #pragma unroll
-            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a0, bq[rn][0], acc[rm][rn]);
-#pragma unroll
-            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a1, bq[rn][1], acc[rm][rn]);
+            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a, bq[rn], acc[rm][rn]);
         }
     };
+    auto no_hook = [](int) {};
 
-    issue_stage(S0{}, 0);
-    if (nk > 1) issue_stage(S1{}, 1);
-    for (int kt = 0; kt < nk; kt += 3) {
-        run_stage(S0{}, kt);
-        if (kt + 1 < nk) run_stage(S1{}, kt + 1);
-        if (kt + 2 < nk) run_stage(S2{}, kt + 2);
+    if constexpr (kPipe == 0) {
+        // stage kt lives in buffer kt % 3; its copies were issued two stages earlier
+        auto run_stage = [&](auto cur, int kt) {
+            constexpr int c = decltype(cur)::value;
+            using Next = std::integral_constant<int, (c + 2) % 3>;
+            if (kt + 1 < nk) wait_vmcnt<kLoadsPerStage>();
+            else wait_vmcnt<0>();
+            stage_barrier();
+            if (kt + 2 < nk) issue_stage(Next{}, kt + 2);
+            uint4 braw[RN];
+            read_b(cur, braw);
+            half_stage(cur, 0, braw, no_hook);
+            half_stage(cur, 1, braw, no_hook);
+        };
+        issue_stage(S0{}, 0);
+        if (nk > 1) issue_stage(S1{}, 1);
+        for (int kt = 0; kt < nk; kt += 3) {
+            run_stage(S0{}, kt);
+            if (kt + 1 < nk) run_stage(S1{}, kt + 1);
+            if (kt + 2 < nk) run_stage(S2{}, kt + 2);
+        }
+    } else {
+        // The barrier that publishes stage kt + 1 sits before the last M
+        // repeat of stage kt's second K half, so stage kt + 1's B operands are
+        // read from LDS while that repeat's MFMAs run; copies for stage kt + 3
+        // then go into stage kt's buffer.
+        issue_stage(S0{}, 0);
+        if (nk > 1) issue_stage(S1{}, 1);
+        if (nk > 2) issue_stage(S2{}, 2);
+        if (nk > 2) wait_vmcnt<2 * kLoadsPerStage>();
+        else if (nk > 1) wait_vmcnt<kLoadsPerStage>();
+        else wait_vmcnt<0>();
+        stage_barrier();
+        uint4 braw[RN];
+        read_b(S0{}, braw);
+        auto run_stage = [&](auto cur, int kt) {
+            constexpr int c = decltype(cur)::value;
+            using Nx = std::integral_constant<int, (c + 1) % 3>;
+            half_stage(cur, 0, braw, no_hook);
+            // half_stage widens braw before running the hook, so the hook may
+            // overwrite braw with the next stage's operands
+            half_stage(cur, 1, braw, [&](int rm) {
+                if (rm == RM - 1 && kt + 1 < nk) {
+                    // every read of this stage has returned; stage kt + 1 has landed
+                    if (kt + 2 < nk) wait_vmcnt_lgkm0<kLoadsPerStage>();
+                    else wait_vmcnt_lgkm0<0>();
+                    stage_barrier();
+                    if (kt + 3 < nk) issue_stage(cur, kt + 3);
+                    read_b(Nx{}, braw);
+                }
+            });
+        };
+        for (int kt = 0; kt < nk; kt += 3) {
+            run_stage(S0{}, kt);
+            if (kt + 1 < nk) run_stage(S1{}, kt + 1);
+            if (kt + 2 < nk) run_stage(S2{}, kt + 2);
+        }
     }
 
     // ---- epilogue (LDS reused after every wave is past its last stage) ----
@@ -247,15 +311,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int PIPE>
 void launch_lds(const MmArgs& p, hipStream_t stream) {
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
-    const int group_m = p.group_m > 0 ? p.group_m : 8;
+    const int group_m = p.group_m > 0 ? p.group_m : 4;
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n));
     const dim3 block(64 * WAVES_M * WAVES_N);
 #define FEATHER_LDS_LAUNCH(BF, E4)                                                                                    \
-    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, BF, E4>), grid, block, 0, stream, p.a, \
+    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4>), grid, block, 0, stream, p.a,   \
                        p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),                      \
                        static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m)
     if (p.out_bf16) {
@@ -268,18 +332,28 @@ void launch_lds(const MmArgs& p, hipStream_t stream) {
 #undef FEATHER_LDS_LAUNCH
 }
 
+template <int PIPE>
+bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream) {
+    switch (kernel_id) {
+        case kLds256x256w2x4: launch_lds<256, 256, 2, 4, PIPE>(p, stream); return true;
+        case kLds256x256w4x2: launch_lds<256, 256, 4, 2, PIPE>(p, stream); return true;
+        case kLds256x128: launch_lds<256, 128, 4, 2, PIPE>(p, stream); return true;
+        case kLds128x256: launch_lds<128, 256, 2, 4, PIPE>(p, stream); return true;
+        case kLds128x128: launch_lds<128, 128, 2, 2, PIPE>(p, stream); return true;
+        default: return false;
+    }
+}
+
 }  // namespace
 
 bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
     if (p.K % kBK != 0) return false;
-    switch (kernel_id) {
-        case kLds256x256w2x4: launch_lds<256, 256, 2, 4, 3>(p, stream); return true;
-        case kLds256x256w4x2: launch_lds<256, 256, 4, 2, 3>(p, stream); return true;
-        case kLds256x128: launch_lds<256, 128, 4, 2, 3>(p, stream); return true;
-        case kLds128x256: launch_lds<128, 256, 2, 4, 3>(p, stream); return true;
-        case kLds128x128: launch_lds<128, 128, 2, 2, 3>(p, stream); return true;
-        default: return false;
-    }
+    // FEATHEROPS_LDS_PIPE: 0 = barrier at the top of each stage, 1 = cross-barrier prefetch
+    static const int pipe_env = [] {
+        const char* e = getenv("FEATHEROPS_LDS_PIPE");
+        return e ? atoi(e) : 0;
+    }();
+    return pipe_env == 0 ? launch_lds_pipe<0>(kernel_id, p, stream) : launch_lds_pipe<1>(kernel_id, p, stream);
 }
 
 }  // namespace feather
