@@ -4,6 +4,10 @@
 // reference for the weight-streaming kernels.
 //
 //   benchmark_hbm_copy [--mib 1024] [--iters 20]
+//   benchmark_hbm_copy --read-sweep   read-only streaming kernel over 16.8 MB,
+//       67 MB and 268 MB buffers, cycling 24 buffers so that the 256 MB
+//       Infinity Cache cannot serve them: the per-call floor a weight-streaming
+//       kernel of that size can reach (launch + ramp + drain included)
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -26,13 +30,61 @@ __global__ __launch_bounds__(256) void copy16(const uint4* __restrict__ src, uin
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
+__global__ __launch_bounds__(256) void read16(const uint4* __restrict__ src, int64_t n, uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * 4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 + threadIdx.x; i < n; i += stride) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i + u * 256 < n ? src[i + u * 256] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live
+}
+
+int read_sweep() {
+    const int nbuf = 24;
+    uint32_t* sink;
+    HIP_OK(hipMalloc(&sink, 4));
+    hipEvent_t t0, t1;
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+    for (const int64_t bytes : {int64_t(16777216), int64_t(67108864), int64_t(268435456)}) {
+        void* bufs[nbuf];
+        for (auto& b : bufs) {
+            HIP_OK(hipMalloc(&b, bytes));
+            HIP_OK(hipMemset(b, 1, bytes));
+        }
+        const int64_t n = bytes / 16;
+        const int grid = 1024;
+        for (int i = 0; i < nbuf; ++i)
+            hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, 0, static_cast<const uint4*>(bufs[i]), n, sink);
+        HIP_OK(hipDeviceSynchronize());
+        HIP_OK(hipEventRecord(t0, 0));
+        for (int i = 0; i < 10 * nbuf; ++i)
+            hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, 0, static_cast<const uint4*>(bufs[i % nbuf]), n, sink);
+        HIP_OK(hipEventRecord(t1, 0));
+        HIP_OK(hipEventSynchronize(t1));
+        float ms = 0.f;
+        HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+        ms /= 10 * nbuf;
+        std::cout << "read " << bytes << " B: " << ms * 1000.0 << " us/call, " << bytes / ms / 1e6 << " GB/s" << std::endl;
+        for (auto& b : bufs) HIP_OK(hipFree(b));
+    }
+    HIP_OK(hipFree(sink));
+    return 0;
+}
+
 int main(int argc, char** argv) {
     int64_t mib = 1024;
     int iters = 20;
-    for (int i = 1; i + 1 < argc; i += 2) {
+    for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
-        if (a == "--mib") mib = std::stoll(argv[i + 1]);
-        else if (a == "--iters") iters = std::stoi(argv[i + 1]);
+        if (a == "--read-sweep") return read_sweep();
+        if (i + 1 >= argc) break;
+        if (a == "--mib") mib = std::stoll(argv[++i]);
+        else if (a == "--iters") iters = std::stoi(argv[++i]);
     }
     const int64_t bytes = mib << 20;
     const int64_t n = bytes / 16;

@@ -6,6 +6,8 @@
 // ms, TFLOP/s and GB/s with GB = 2*M*K + N*K + 2*M*N bytes. Inputs follow the
 // same recipe (A uniform in [-1, 1) from mt19937(42); B drawn from the nine
 // e5m2 codes {0, +-0.25, +-0.5, +-0.75, +-1}; scale 2.34; bias uniform).
+// Calls go through feather_launch_scaled_mm_ws with the workspace the call
+// can use (the small-M split-K path), allocated once and reused.
 // Additions: --out fp16|bf16, --rotate R (cycle through R distinct weight
 // buffers so that a weight larger than the 256 MB Infinity Cache in total is
 // streamed from HBM), --b e5m2|e4m3. Default config is the gfx950 256x256
@@ -139,6 +141,14 @@ int main(int argc, char** argv) {
     const float hs = 2.34f;
     HIP_OK(hipMemcpy(dscale, &hs, sizeof(float), hipMemcpyHostToDevice));
 
+    // workspace for the small-M split-K path (zero-filled, reused by every call)
+    const size_t ws_bytes = feather_scaled_mm_workspace_size(o.m, o.n, o.k, o.wm, o.wn, o.u, o.rm, o.rn);
+    void* dws = nullptr;
+    if (ws_bytes) {
+        HIP_OK(hipMalloc(&dws, ws_bytes));
+        HIP_OK(hipMemset(dws, 0, ws_bytes));
+    }
+
     hipStream_t stream;
     hipEvent_t t0, t1;
     HIP_OK(hipStreamCreate(&stream));
@@ -146,9 +156,9 @@ int main(int argc, char** argv) {
     HIP_OK(hipEventCreate(&t1));
 
     auto run = [&](int i) {
-        const bool ok = launch_scaled_mm(da, db[i % o.rotate], dscale, static_cast<const uint16_t*>(dbias),
-                                         static_cast<uint16_t*>(dc), o.m, o.n, o.k, 1, 1, o.wm, o.wn, o.u, o.rm, o.rn,
-                                         o.b_dtype, o.out_bf16, stream);
+        const bool ok = feather_launch_scaled_mm_ws(da, db[i % o.rotate], dscale, static_cast<const uint16_t*>(dbias),
+                                                    static_cast<uint16_t*>(dc), o.m, o.n, o.k, 1, 1, o.wm, o.wn, o.u,
+                                                    o.rm, o.rn, o.b_dtype, o.out_bf16, dws, ws_bytes, stream);
         if (!ok) {
             std::cerr << "Failed to launch kernel: unsupported config" << std::endl;
             std::exit(1);
@@ -199,6 +209,7 @@ int main(int argc, char** argv) {
     HIP_OK(hipEventDestroy(t1));
     HIP_OK(hipStreamDestroy(stream));
     for (auto p : db) HIP_OK(hipFree(p));
+    if (dws) HIP_OK(hipFree(dws));
     HIP_OK(hipFree(da));
     HIP_OK(hipFree(dbias));
     HIP_OK(hipFree(dc));

@@ -67,6 +67,16 @@ int tuning_group_m() {
     return g;
 }
 
+// FEATHEROPS_SMALLM_GROUPS: workgroup count the small-M K split aims for (tuning knob, default 256).
+int tuning_smallm_groups() {
+    static const int g = [] {
+        const char* e = getenv("FEATHEROPS_SMALLM_GROUPS");
+        const int v = e ? atoi(e) : 256;
+        return v > 0 ? v : 256;
+    }();
+    return g;
+}
+
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
 }  // namespace
@@ -80,10 +90,18 @@ int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps
     return kernel_for(M, K, block_warps_m, block_warps_n, repeat_m, repeat_n);
 }
 
-bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,
-                      int64_t M, int64_t N, int64_t K, int has_scale, int has_bias, int block_warps_m,
-                      int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype, int output_dtype,
-                      hipStream_t stream) {
+size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
+                                        int unroll_k, int repeat_m, int repeat_n) {
+    const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    if (kid != feather::kSmallM) return 0;
+    return feather::smallm_workspace_bytes(M, N, K, tuning_smallm_groups());
+}
+
+bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                                 uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                                 int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                 int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
     const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
     if (kid == feather::kKernelNone) return false;
     if (b_dtype != FEATHER_B_E4M3FN && b_dtype != FEATHER_B_E5M2) return false;
@@ -103,9 +121,19 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
     p.out_bf16 = output_dtype == 1;
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
     p.group_m = tuning_group_m();
-    if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, stream);
+    p.smallm_min_groups = tuning_smallm_groups();
+    if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
     if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
+}
+
+bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,
+                      int64_t M, int64_t N, int64_t K, int has_scale, int has_bias, int block_warps_m,
+                      int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype, int output_dtype,
+                      hipStream_t stream) {
+    return feather_launch_scaled_mm_ws(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias, block_warps_m,
+                                       block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype, output_dtype, nullptr, 0,
+                                       stream);
 }
 
 int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,

@@ -18,6 +18,7 @@ struct MmArgs {
     bool out_bf16;
     bool b_e4m3;
     int group_m;             // tile raster group height (0 = default)
+    int smallm_min_groups;   // small-M: workgroup count the K split aims for (0 = default)
 };
 
 // Kernel variants. Values are stable: the Python autotuner de-duplicates
@@ -40,7 +41,13 @@ enum KernelId : int {
 };
 
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
-bool launch_smallm_kernel(const MmArgs& p, hipStream_t stream);
+// Small-M kernel. With a workspace of at least smallm_workspace_bytes() it
+// also splits K across workgroups; without one it splits K inside each
+// workgroup only. The workspace's first bytes are arrival counters that must
+// be zero before the first call; every call leaves them zero again.
+bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups);
+int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups);
 bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
 
 }  // namespace feather

@@ -1,19 +1,26 @@
 // Small-M (M <= 64) fp16 x fp8 GEMM for gfx950: the weight-streaming regime.
 //
-// Same contract as the tile kernel (reference kernel/hip/hip_kernel.cu:133-420:
+// Same contract as the tile kernels (reference kernel/hip/hip_kernel.cu:133-420:
 // fp32 accumulation, scale on the accumulator, rounding to the output type,
 // bias added in the output type). At M <= 64 the weight bytes dominate HBM
 // traffic (M=16, K=N=4096: 16.8 MB of weight vs 0.26 MB of activations and
 // output), so the kernel is built to stream Bp once at full bandwidth:
-//   * one workgroup per 16-column strip of N, 16 waves splitting K between
-//     them (split-K inside the workgroup); every wave keeps several 64-K stages
-//     of 16-byte weight loads in flight;
+//   * a workgroup owns a strip of 16 * CT columns and one of `ksplit` K
+//     ranges; its 16 waves split that K range again and keep several 64-K
+//     stages of 16-byte weight loads in flight each;
+//   * a wave reuses each A fragment for its CT column tiles, so activations
+//     are re-read from L2 once per 16 * CT columns (not once per 16);
 //   * the contraction of each 16 x 64 slice runs on the 16x16x32 fp16 MFMA:
 //     the wave64 VALU (v_dot2_f32_f16: 256 flop/clk/CU, 157 TFLOP/s chip-wide)
-//     would need 3.4 us for M=16, K=N=4096, above the 3.0 us budget of 70% of
-//     HBM bandwidth, while the MFMA does it in a fraction of the load time;
-//   * partial sums of the 16 waves are reduced through LDS in a fixed order
-//     (deterministic), then the epilogue applies scale, rounding and bias.
+//     would need 3.4 us for M=16, K=N=4096, more than the whole weight stream;
+//   * the 16 waves' partial sums are reduced through LDS in a fixed order;
+//   * with ksplit > 1 each workgroup stores its fp32 partial in a caller
+//     workspace and bumps the strip's arrival counter; the workgroup that
+//     arrives last adds the ksplit partials in split order (deterministic,
+//     no waiting on other workgroups), applies the epilogue and re-zeroes the
+//     counter for the next call. Partials and counters use device-coherent
+//     (agent-scope) loads, stores and atomics; the splits of a strip are also
+//     placed on one XCD (workgroup p runs on XCD p % 8).
 #include "feather_common.h"
 #include "scaled_mm_dispatch.h"
 
@@ -22,38 +29,63 @@ namespace {
 
 constexpr int kWaves = 16;
 
-template <int MT, bool kBf16, bool kE4m3>
+template <int MT, int CT, bool kBf16, bool kE4m3>
 __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias) {
-    constexpr int U = MT <= 2 ? 4 : 2;  // stages in flight per wave
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
+    int nstrips, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters) {
+    constexpr int U = (MT * 2 + CT) <= 4 ? 4 : 2;  // stages in flight per wave
     constexpr int kRows = MT * 16;
-    constexpr int kRedStride = 17;      // floats per reduction row (16 + 1 pad)
+    constexpr int kCols = CT * 16;
+    constexpr int kRedStride = kCols + 1;  // floats per reduction row (+1 pad)
     __shared__ float red[kWaves][kRows][kRedStride];
+    __shared__ int last_flag;
+
+    // ---- workgroup -> (strip, K split); splits of a strip share an XCD ----
+    const int pid = blockIdx.x;
+    int strip, q;
+    if (nstrips % kNumXcd == 0) {
+        const int j = pid / kNumXcd;
+        q = j % ksplit;
+        strip = (j / ksplit) * kNumXcd + pid % kNumXcd;
+    } else {
+        strip = pid / ksplit;
+        q = pid % ksplit;
+    }
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const int col = n0 + lr;
+    const int n0 = strip * kCols;
     const int kgroups = K >> 4;
     const int nst = (K + 63) >> 6;
+    const int per_split = (nst + ksplit - 1) / ksplit;
+    const int st_begin = q * per_split;
+    const int st_end = st_begin + per_split < nst ? st_begin + per_split : nst;
 
-    f32x4 acc[MT];
+    f32x4 acc[MT][CT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int base = wave; base < nst; base += kWaves * U) {
-        uint4 braw[U];
+    for (int base = st_begin + wave; base < st_end; base += kWaves * U) {
+        uint4 braw[U][CT];
         uint4 araw[U][MT][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int kg = (base + u * kWaves) * 4 + lg;
-            const bool kval = kg < kgroups;
-            braw[u] = kval ? *reinterpret_cast<const uint4*>(Bp + (static_cast<int64_t>(kg) * N + col) * 16)
-                           : make_uint4(0u, 0u, 0u, 0u);
+            const int st = base + u * kWaves;
+            const int kg = st * 4 + lg;
+            const bool kval = st < st_end && kg < kgroups;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const int col = n0 + ct * 16 + lr;
+                braw[u][ct] = (kval && col < N)
+                                  ? *reinterpret_cast<const uint4*>(Bp + (static_cast<int64_t>(kg) * N + col) * 16)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int row = mt * 16 + lr;
@@ -69,13 +101,16 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (base + u * kWaves < nst) {
-                const half8_t b0 = widen_fp8x8<kE4m3>(braw[u].x, braw[u].y);
-                const half8_t b1 = widen_fp8x8<kE4m3>(braw[u].z, braw[u].w);
+            if (base + u * kWaves < st_end) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    acc[mt] = mfma16x16x32(as_half8(araw[u][mt][0]), b0, acc[mt]);
-                    acc[mt] = mfma16x16x32(as_half8(araw[u][mt][1]), b1, acc[mt]);
+                for (int ct = 0; ct < CT; ++ct) {
+                    const half8_t b0 = widen_fp8x8<kE4m3>(braw[u][ct].x, braw[u][ct].y);
+                    const half8_t b1 = widen_fp8x8<kE4m3>(braw[u][ct].z, braw[u][ct].w);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        acc[mt][ct] = mfma16x16x32(as_half8(araw[u][mt][0]), b0, acc[mt][ct]);
+                        acc[mt][ct] = mfma16x16x32(as_half8(araw[u][mt][1]), b1, acc[mt][ct]);
+                    }
                 }
             }
         }
@@ -85,30 +120,83 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave][mt * 16 + 4 * lg + i][lr] = acc[mt][i];
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][mt * 16 + 4 * lg + i][ct * 16 + lr] = acc[mt][ct][i];
     __syncthreads();
 
-    const float s = has_scale ? scale[0] : 1.0f;
-    for (int e = tid; e < M * 16; e += 64 * kWaves) {
-        const int r = e >> 4;
-        const int c = e & 15;
-        float sum = 0.f;
+    const int tile_elems = M * kCols;
+    if (ksplit > 1) {
+        // Partials are written and read with agent-scope (device-coherent)
+        // accesses, so no cache-wide write-back or invalidate is needed: the
+        // vmcnt wait makes every store of this workgroup complete before the
+        // arrival count is bumped, and the last arrival reads the partials
+        // straight from the coherent level.
+        float* my_part = partials + (static_cast<int64_t>(strip) * ksplit + q) * tile_elems;
+        for (int e = tid; e < tile_elems; e += 64 * kWaves) {
+            float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) sum += red[w][r][c];
+            for (int w = 0; w < kWaves; ++w) sum += red[w][e / kCols][e % kCols];
+            __hip_atomic_store(&my_part[e], sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if (tid == 0)
+            last_flag = __hip_atomic_fetch_add(&counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        static_cast<uint32_t>(ksplit - 1);
+        __syncthreads();
+        if (!last_flag) return;
+    }
+
+    const float s = has_scale ? scale[0] : 1.0f;
+    for (int e = tid; e < tile_elems; e += 64 * kWaves) {
+        const int r = e / kCols;
+        const int c = e % kCols;
+        if (n0 + c >= N) continue;
+        float sum = 0.f;
+        if (ksplit > 1) {
+            const float* strip_parts = partials + static_cast<int64_t>(strip) * ksplit * tile_elems;
+            for (int qq = 0; qq < ksplit; ++qq)
+                sum += __hip_atomic_load(&strip_parts[static_cast<int64_t>(qq) * tile_elems + e], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) sum += red[w][r][c];
+        }
         const float v = kE4m3 ? (sum * 256.0f) * s : sum * s;
         uint16_t o = f32_to_out_bits<kBf16>(v);
         if (has_bias) o = f32_to_out_bits<kBf16>(out_bits_to_f32<kBf16>(o) + out_bits_to_f32<kBf16>(bias[n0 + c]));
         C[static_cast<int64_t>(r) * N + n0 + c] = o;
     }
+    if (ksplit > 1 && tid == 0)  // ready for the next call on this stream
+        __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int MT>
-void launch_mt(const MmArgs& p, hipStream_t stream) {
-    const dim3 grid(static_cast<uint32_t>(p.N / 16));
+// Shape policy (measured on MI355X, M=16..64, weights rotated past the MALL):
+//   * K is split across workgroups only for M > 32, where the activation
+//     re-reads dominate; for M <= 32 the arrival/reduction round trip costs
+//     more than it saves;
+//   * without a workgroup K split, strips are widened to 64 columns only when
+//     that still leaves >= 192 workgroups (N >= 12288), otherwise every CU is
+//     needed and strips stay 16 columns wide.
+constexpr int kSplitMinMt = 3;
+constexpr int kWideStripMinGroups = 192;
+constexpr int ct_split(int mt) { return mt <= 2 ? 4 : 2; }
+
+int ct_unsplit(int mt, int64_t N) {
+    if (mt <= 2 && (N + 63) / 64 >= kWideStripMinGroups) return 4;
+    return 1;
+}
+
+template <int MT, int CT>
+void launch_mt(const MmArgs& p, int ksplit, float* partials, uint32_t* counters, hipStream_t stream) {
+    const int nstrips = static_cast<int>((p.N + 16 * CT - 1) / (16 * CT));
+    const dim3 grid(static_cast<uint32_t>(nstrips * ksplit));
     const dim3 block(64 * kWaves);
-#define FEATHER_SMALLM_LAUNCH(BF, E4)                                                                                 \
-    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, BF, E4>), grid, block, 0, stream, p.a, p.b, p.scale, p.bias, p.c, \
-                       static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K), p.has_scale, p.has_bias)
+#define FEATHER_SMALLM_LAUNCH(BF, E4)                                                                       \
+    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, CT, BF, E4>), grid, block, 0, stream, p.a, p.b, p.scale, \
+                       p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),     \
+                       p.has_scale, p.has_bias, nstrips, ksplit, partials, counters)
     if (p.out_bf16) {
         if (p.b_e4m3) FEATHER_SMALLM_LAUNCH(true, true);
         else FEATHER_SMALLM_LAUNCH(true, false);
@@ -119,16 +207,58 @@ void launch_mt(const MmArgs& p, hipStream_t stream) {
 #undef FEATHER_SMALLM_LAUNCH
 }
 
+int mt_of(int64_t M) { return static_cast<int>((M + 15) / 16); }
+
 }  // namespace
 
-bool launch_smallm_kernel(const MmArgs& p, hipStream_t stream) {
+int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups) {
+    if (M <= 0 || M > 64 || mt_of(M) < kSplitMinMt) return 1;
+    const int ct = ct_split(mt_of(M));
+    const int64_t nstrips = (N + 16 * ct - 1) / (16 * ct);
+    const int64_t nst = (K + 63) / 64;
+    int64_t ks = (target_groups + nstrips - 1) / nstrips;
+    // each split keeps at least one 64-K stage per wave
+    const int64_t max_ks = nst / kWaves > 0 ? nst / kWaves : 1;
+    if (ks > max_ks) ks = max_ks;
+    if (ks > 8) ks = 8;
+    return ks < 1 ? 1 : static_cast<int>(ks);
+}
+
+size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups) {
+    const int ks = smallm_ksplit(M, N, K, target_groups);
+    if (ks <= 1) return 0;
+    const int ct = ct_split(mt_of(M));
+    const int64_t nstrips = (N + 16 * ct - 1) / (16 * ct);
+    // counters first (256-byte aligned), then ksplit partial tiles per strip
+    const size_t counter_bytes = (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256;
+    return counter_bytes + static_cast<size_t>(nstrips) * ks * M * 16 * ct * 4;
+}
+
+bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (p.M <= 0 || p.M > 64) return false;
-    const int mt = static_cast<int>((p.M + 15) / 16);
+    const int mt = mt_of(p.M);
+    const int target = p.smallm_min_groups > 0 ? p.smallm_min_groups : 256;
+    int ks = smallm_ksplit(p.M, p.N, p.K, target);
+    if (ks > 1 && (workspace == nullptr || workspace_bytes < smallm_workspace_bytes(p.M, p.N, p.K, target)))
+        ks = 1;  // no (or too small a) workspace: split K inside each workgroup only
+    if (ks > 1) {
+        const int ct = ct_split(mt);
+        const int64_t nstrips = (p.N + 16 * ct - 1) / (16 * ct);
+        uint32_t* counters = static_cast<uint32_t*>(workspace);
+        float* partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                                   (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256);
+        switch (mt) {
+            case 3: launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream); return true;
+            case 4: launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream); return true;
+            default: return false;
+        }
+    }
+    const bool wide = ct_unsplit(mt, p.N) == 4;
     switch (mt) {
-        case 1: launch_mt<1>(p, stream); return true;
-        case 2: launch_mt<2>(p, stream); return true;
-        case 3: launch_mt<3>(p, stream); return true;
-        case 4: launch_mt<4>(p, stream); return true;
+        case 1: wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream); return true;
+        case 2: wide ? launch_mt<2, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<2, 1>(p, 1, nullptr, nullptr, stream); return true;
+        case 3: launch_mt<3, 1>(p, 1, nullptr, nullptr, stream); return true;
+        case 4: launch_mt<4, 1>(p, 1, nullptr, nullptr, stream); return true;
         default: return false;
     }
 }

@@ -26,6 +26,9 @@ _vp = ctypes.c_void_p
 SIGNATURES: dict[str, tuple] = {
     "launch_scaled_mm": (ctypes.c_bool, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _int,
                                          _int, _int, _int, _int, _vp]),
+    "feather_launch_scaled_mm_ws": (ctypes.c_bool, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int,
+                                                    _int, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]),
+    "feather_scaled_mm_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "feather_scaled_mm_kernel_id": (_int, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "feather_quantize_prepack_e5m2": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp]),
     "feather_quantize_prepack_e5m2_scaled": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),

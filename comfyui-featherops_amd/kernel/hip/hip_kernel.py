@@ -89,21 +89,43 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     _check(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit")
 
 
+# Per-(device, stream) workspaces for the small-M split-K kernel. They start
+# zero-filled and every call leaves their counter words zero again; keying by
+# stream keeps concurrent streams on separate workspaces.
+_WORKSPACES: dict = {}
+
+
+def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (dev.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _scaled_mm_native(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
                       b_dtype) -> None:
     validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
                        b_dtype)
     L = _lib.lib()
     dev = a.device
+    M, K = a.shape
+    N = b_prepacked.shape[1]
     with torch.cuda.device(dev):
-        launched = L.launch_scaled_mm(
+        stream = _lib.stream_ptr(dev)
+        ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m,
+                                                      repeat_n)
+        ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
+        launched = L.feather_launch_scaled_mm_ws(
             a.data_ptr(), b_prepacked.data_ptr(),
             scale.data_ptr() if scale is not None else None,
             bias.data_ptr() if bias is not None else None,
-            c.data_ptr(), a.shape[0], b_prepacked.shape[1], a.shape[1],
+            c.data_ptr(), M, N, K,
             1 if scale is not None else 0, 1 if bias is not None else 0,
             block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
-            0 if c.dtype == torch.float16 else 1, _lib.stream_ptr(dev))
+            0 if c.dtype == torch.float16 else 1,
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
     _check(bool(launched), "Unsupported config")
 
 

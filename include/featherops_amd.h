@@ -19,6 +19,7 @@
 
 #include <hip/hip_runtime_api.h>
 #include <stdbool.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -58,6 +59,27 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
                       uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias, int block_warps_m,
                       int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype, int output_dtype,
                       hipStream_t stream);
+
+/*
+ * launch_scaled_mm with a caller workspace. For small M (M <= 64) the kernel
+ * then also splits K across workgroups, which the weight-streaming regime
+ * needs to keep every CU loading (the reference ABI has no workspace, so
+ * launch_scaled_mm splits K inside each workgroup only). workspace_bytes must
+ * be at least feather_scaled_mm_workspace_size(...) (0 means none needed; a
+ * smaller workspace falls back to the unsplit kernel). The workspace must be
+ * zero-filled before its first use and is left zero-filled by every call;
+ * calls that run concurrently need distinct workspaces. No counterpart in the
+ * reference; the torch op binding uses it.
+ */
+bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                                 uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                                 int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                 int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
+/* Workspace bytes feather_launch_scaled_mm_ws can use for this call (0 = none). */
+size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
+                                        int unroll_k, int repeat_m, int repeat_n);
 
 /*
  * Which gfx950 kernel launch_scaled_mm would run for this shape and

@@ -108,3 +108,29 @@ def test_torch_compile_configured_and_autotuned(cuda, hk):
     ref2 = O.scaled_mm_ref(xv.to(torch.float16).view(-1, 512).cpu().numpy(), bp.view(torch.uint8).cpu().numpy(),
                            None, bias.cpu().numpy(), O.DT_F16)
     assert_gemm_close(y, ref2, torch.float16, "compile autotuned view input no scale")
+
+
+def test_graph_capture_replays_match_eager(cuda, hk, quant):
+    """scaled_mm (small-M and tile kernels) and quantize captured in a HIP graph:
+    every replay, with eager work in between, equals the eager result."""
+    g = torch.Generator(device=cuda).manual_seed(3)
+    w = (torch.randn(512, 1024, generator=g, device=cuda) * 0.02).half()
+    qt = quant.make_feather_quantized_weight(w, None, torch.float16)
+    bp, scale = quant.get_feather_plain_tensors(qt)
+    bias = (torch.randn(512, generator=g, device=cuda) * 0.01).half()
+    for m, cfg in ((16, (1, 1, 2, 1, 2)), (512, (2, 4, 4, 8, 4))):
+        a = torch.randn(m, 1024, generator=g, device=cuda).half()
+        eager = hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg)
+        out = torch.empty_like(eager)
+        hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg)  # warm the op before capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out.copy_(hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg))
+        for rep in range(4):
+            out.zero_()
+            graph.replay()
+            junk = torch.randn(1 << 16, device=cuda).sum()  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {rep} m={m}"
+            assert torch.isfinite(junk)

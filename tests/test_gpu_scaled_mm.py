@@ -174,3 +174,35 @@ def test_baseline_config3_image_dit(cuda, K, N):
 @pytest.mark.parametrize("K,N", [(5120, 13824), (13824, 5120), (5120, 5120)])
 def test_baseline_config4_video_dit(cuda, K, N):
     _sampled_rows_check(cuda, 32768, N, K, torch.float16, (2, 4, 4, 8, 4), nrows=16)
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (16, 3072, 3072), (1, 1040, 2048), (33, 2000, 4096),
+                                   (64, 4096, 4096), (48, 12288, 2048), (16, 128, 128)])
+def test_small_m_split_k_workspace(cuda, M, N, K):
+    """feather_launch_scaled_mm_ws: K split across workgroups through the
+    workspace; twice in a row (the arrival counters must come back to zero)."""
+    from gpu_util import lib, stream
+
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).half()
+    packed, s = weight_like(N, K, g)
+    bias, bias_np = _bias_for(torch.float16, N, g)
+    ref = O.scaled_mm_ref(a.numpy(), packed, s, bias_np, O.DT_F16)
+    cfg = (1, 1, 2, 1, 2)
+    nbytes = lib().feather_scaled_mm_workspace_size(M, N, K, *cfg)
+    ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=cuda)
+    ad, bd, sd, bsd = a.to(cuda), to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), bias.to(cuda)
+    outs = []
+    for _ in range(2):
+        c = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
+        ok = lib().feather_launch_scaled_mm_ws(ad.data_ptr(), bd.data_ptr(), sd.data_ptr(), bsd.data_ptr(),
+                                               c.data_ptr(), M, N, K, 1, 1, *cfg, 1, 0, ws.data_ptr(), ws.numel(),
+                                               stream(cuda))
+        assert ok
+        torch.cuda.synchronize()
+        assert_gemm_close(c, ref, torch.float16, f"ws {M}x{N}x{K}")
+        outs.append(c)
+    assert torch.equal(outs[0], outs[1]), "split-K reduction must be deterministic"
+    if nbytes:  # split across workgroups (M > 32): 32-column strips, one counter each
+        strips = (N + 31) // 32
+        assert (ws[: strips * 4] == 0).all(), "arrival counters must be left at zero"
