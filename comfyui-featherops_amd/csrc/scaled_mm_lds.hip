@@ -55,11 +55,13 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// A rows are 128 bytes (8 chunks of 16 B). A ds_read_b128 of 16 rows (lanes
-// 0-15, same logical chunk) is served 256 bytes (64 banks) per cycle: rows r
-// and r + 1 share a 256-byte bank row, so rows of equal parity get distinct
-// chunks.
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+// A rows are 128 bytes (8 chunks of 16 B); chunk c of row r sits at c ^ swz(r).
+// An A-operand ds_read_b128 has lanes 0-15 on 16 consecutive rows (one
+// logical chunk) and lanes 16-31 / 32-47 / 48-63 on the same rows at other
+// chunks. Measured on gfx950 with SQ_LDS_BANK_CONFLICT: r & 7 and
+// (r >> 1) & 7 both take 8 LDS cycles per instruction (2-way conflicts), while
+// (r & 7) ^ ((r >> 3) & 1) takes the conflict-free 4.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 // 16 bytes per lane from sbase + voff into LDS at lds_dst + 16 * lane
 // (sbase and lds_dst wave-uniform). Inline asm so that the compiler's
@@ -202,14 +204,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // every M repeat. `hook(rm)` runs before the MFMAs of repeat rm.
     auto half_stage = [&](auto cur, int kh, const uint4 (&braw)[RN], auto hook) {
         const uint8_t* sa = stage_buf(cur);
+        // all M repeats' A operands are requested up front so that LDS latency
+        // overlaps the MFMAs of the earlier repeats
+        uint4 araw[RM];
+#pragma unroll
+        for (int rm = 0; rm < RM; ++rm) araw[rm] = *reinterpret_cast<const uint4*>(sa + a_lds(rm, kh));
         half8_t bq[RN];
 #pragma unroll
         for (int rn = 0; rn < RN; ++rn)
             bq[rn] = kh == 0 ? widen_fp8x8<kE4m3>(braw[rn].x, braw[rn].y) : widen_fp8x8<kE4m3>(braw[rn].z, braw[rn].w);
 #pragma unroll
         for (int rm = 0; rm < RM; ++rm) {
-            const half8_t a = as_half8(*reinterpret_cast<const uint4*>(sa + a_lds(rm, kh)));
             hook(rm);
+            const half8_t a = as_half8(araw[rm]);
 #pragma unroll
             for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a, bq[rn], acc[rm][rn]);
         }
