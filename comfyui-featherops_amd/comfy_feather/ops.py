@@ -5,9 +5,13 @@ ComfyUI's `custom_operations` hook whose `Linear`:
   * at state-dict load quantizes the weight to prepacked e5m2 on the GPU
     (make_feather_quantized_weight) unless the layer is excluded, 1-wide, or
     has in_features % 16 != 0 (ops.py:31-64);
-  * in forward pads the flattened M to a multiple of 16/32/64/128, casts x to
-    fp16, runs scaled_mm_hip with the weight scale and bias, casts back to the
-    input dtype, slices, and applies basic LoRA patches (ops.py:85-146).
+  * in forward casts x to fp16, runs the scaled_mm kernel with the weight
+    scale and bias, casts back to the input dtype and applies basic LoRA
+    patches (ops.py:85-146). The reference pads the flattened M to a multiple
+    of 16/32/64/128 (a copy) and slices the result (another copy) because its
+    kernel has no row masking; the gfx950 kernels mask rows past M, so by
+    default M is passed as is (`pad_m=True` on the class restores the
+    reference's padding + autotuned scaled_mm_hip call).
 
 Inside ComfyUI it subclasses comfy.ops.manual_cast. Without ComfyUI, a
 minimal base (plain nn.Linear; weight/bias used as stored) stands in so the
@@ -20,7 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel.hip.hip_kernel import scaled_mm_hip
+from ..kernel.hip.hip_kernel import scaled_mm_hip, scaled_mm_hip_any_m
 from .lora import apply_lora_patches
 from .quant import (
     HAVE_COMFY,
@@ -89,6 +93,8 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
         _out_dtype = out_dtype
 
         class Linear(manual_cast.Linear):
+            pad_m = False
+
             def __init__(self, *args, **kwargs):
                 super().__init__(*args, **kwargs)
                 self.excluded_names = FeatherOps._excluded_names
@@ -150,7 +156,10 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                                                                 bias_dtype=bias_dtype, offloadable=True)
                 weight, scale = get_feather_plain_tensors(weight)
                 scale = scale.to(device=x.device, dtype=torch.float32)
-                y = scaled_mm_hip(x, weight, scale, bias, out_dtype=self.out_dtype)
+                if self.pad_m:
+                    y = scaled_mm_hip(x, weight, scale, bias, out_dtype=self.out_dtype)
+                else:
+                    y = scaled_mm_hip_any_m(x, weight, scale, bias, self.out_dtype)
                 uncast_bias_weight(self, weight, bias, offload_stream)
                 self.weight_function = saved_weight_function
                 return y.to(dtype_orig)
@@ -170,10 +179,13 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                 m = x.shape[0]
                 if m == 0:
                     return x.new_empty(*shape[:-1], self.out_features)
-                block = _m_block(m)
-                m_padded = (m + block - 1) // block * block
-                x_padded = F.pad(x, (0, 0, 0, m_padded - m)) if m_padded != m else x
-                y = self._forward_padded(x_padded)[:m]
+                if self.pad_m:
+                    block = _m_block(m)
+                    m_padded = (m + block - 1) // block * block
+                    x_padded = F.pad(x, (0, 0, 0, m_padded - m)) if m_padded != m else x
+                    y = self._forward_padded(x_padded)[:m]
+                else:
+                    y = self._forward_padded(x)
                 y = apply_lora_patches(x, y, self.weight_function)
                 return y.view(*shape[:-1], y.shape[-1])
 

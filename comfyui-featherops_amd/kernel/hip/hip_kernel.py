@@ -32,9 +32,12 @@ def _check(cond: bool, msg: str) -> None:
 
 
 def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
-                       b_dtype, require_cuda: bool = True) -> None:
+                       b_dtype, require_cuda: bool = True, block_divisible: bool = True) -> None:
     """Raise RuntimeError with the reference's message for any argument the
-    kernel cannot take. `require_cuda=False` skips the device checks."""
+    kernel cannot take. `require_cuda=False` skips the device checks;
+    `block_divisible=False` replaces the BlockM/BlockN/ChunkK divisibility
+    rules by what the gfx950 kernels need (N % 16 == 0; K % 16 is always
+    required) -- the any-M entry."""
     if require_cuda:
         _check(a.is_cuda, "a must be a CUDA tensor")
         _check(b_prepacked.is_cuda, "b_prepacked must be a CUDA tensor")
@@ -83,9 +86,12 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     block_m = 16 * block_warps_m * repeat_m
     block_n = 16 * block_warps_n * repeat_n
     chunk_k = 16 * unroll_k
-    _check(M % block_m == 0, f"M ({M}) must be divisible by kBlockM ({block_m})")
-    _check(N % block_n == 0, f"N ({N}) must be divisible by kBlockN ({block_n})")
-    _check(K % chunk_k == 0, f"K ({K}) must be divisible by kChunkK ({chunk_k})")
+    if block_divisible:
+        _check(M % block_m == 0, f"M ({M}) must be divisible by kBlockM ({block_m})")
+        _check(N % block_n == 0, f"N ({N}) must be divisible by kBlockN ({block_n})")
+        _check(K % chunk_k == 0, f"K ({K}) must be divisible by kChunkK ({chunk_k})")
+    else:
+        _check(N % 16 == 0, f"N ({N}) must be divisible by 16")
     _check(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit")
 
 
@@ -254,6 +260,63 @@ def scaled_mm_hip(
     best_cfg = old_autotune(M, N, K, _CONFIGS, run_fn, "mixed", b_prepacked.dtype, out_dtype,
                             kernel_id=lambda cfg: kernel_id(M, N, K, cfg))
     return _configured_op(a, b_prepacked, scale, bias, out_dtype, *best_cfg)
+
+
+# ---------------------------------------------------------------------------
+# any-M entry (no M padding): the gfx950 kernels mask rows past M
+# ---------------------------------------------------------------------------
+
+# (small-M kernel, 256x256 tile) picked by M; their tuples are in _CONFIGS
+_ANY_M_SMALL = (1, 1, 2, 1, 2)
+_ANY_M_LARGE = (2, 4, 4, 8, 4)
+
+
+def any_m_config(M: int) -> tuple:
+    return _ANY_M_SMALL if M <= 64 else _ANY_M_LARGE
+
+
+@torch.library.custom_op("feather_ops_internal::scaled_mm_any_m", mutates_args=())
+def _any_m_op(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    M, K = a.shape
+    N = b_prepacked.shape[1]
+    out = torch.empty((M, N), device=a.device, dtype=out_dtype)
+    if M == 0:
+        return out
+    cfg = any_m_config(M)
+    validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, 0 if b_prepacked.dtype == torch.float8_e4m3fn else 1,
+                       block_divisible=False)
+    L = _lib.lib()
+    dev = a.device
+    with torch.cuda.device(dev):
+        stream = _lib.stream_ptr(dev)
+        ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
+        ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
+        launched = L.feather_launch_scaled_mm_ws(
+            a.data_ptr(), b_prepacked.data_ptr(), scale.data_ptr() if scale is not None else None,
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), M, N, K,
+            1 if scale is not None else 0, 1 if bias is not None else 0, *cfg,
+            0 if b_prepacked.dtype == torch.float8_e4m3fn else 1, 0 if out_dtype == torch.float16 else 1,
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
+    _check(bool(launched), "Unsupported config")
+    return out
+
+
+@_any_m_op.register_fake
+def _(a, b_prepacked, scale, bias, out_dtype):
+    return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+
+
+def scaled_mm_hip_any_m(a, b_prepacked, scale, bias, out_dtype) -> torch.Tensor:
+    """scaled_mm for any row count M, without padding A or slicing C (the
+    kernels mask rows past M). Rows are independent, so the result equals
+    padding M to a block multiple, calling scaled_mm_hip and slicing."""
+    return _any_m_op(a, b_prepacked, scale, bias, out_dtype)
 
 
 def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:

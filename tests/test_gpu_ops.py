@@ -20,15 +20,17 @@ def _linear_ref(x: torch.Tensor, qdata: torch.Tensor, scale: float, bias, out_dt
     return O.scaled_mm_ref(a, qdata.view(torch.uint8).cpu().numpy(), np.float32(scale), b, od)
 
 
+@pytest.mark.parametrize("pad_m", [False, True])
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [1, 37, 130, 300])
-def test_feather_linear_forward(cuda, pkg, out_dtype, m):
+def test_feather_linear_forward(cuda, pkg, out_dtype, m, pad_m):
     from featherops_amd.comfy_feather import ops, quant
 
     g = torch.Generator().manual_seed(m)
     K, N = 256, 384
     ops_cls = ops.feather_ops(out_dtype=out_dtype)
     lin = ops_cls.Linear(K, N)
+    lin.pad_m = pad_m
     sd = {"weight": (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16),
           "bias": (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)}
     lin._load_from_state_dict(sd, "", {}, True, [], [], [])
@@ -44,7 +46,7 @@ def test_feather_linear_forward(cuda, pkg, out_dtype, m):
     # the layer casts its out_dtype result back to the input dtype (bf16)
     ref_t = torch.from_numpy(O.bf16_bits_to_f32(ref) if ref.dtype == np.uint16 else ref.astype(np.float32))
     ref_bf = ref_t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
-    assert_gemm_close(y.reshape(-1, N), ref_bf, torch.bfloat16, f"linear m={m}")
+    assert_gemm_close(y.reshape(-1, N), ref_bf, torch.bfloat16, f"linear m={m} pad_m={pad_m}")
 
 
 def test_feather_linear_excluded_and_patch(cuda, pkg):
@@ -134,3 +136,23 @@ def test_graph_capture_replays_match_eager(cuda, hk, quant):
             torch.cuda.synchronize()
             assert torch.equal(out, eager), f"replay {rep} m={m}"
             assert torch.isfinite(junk)
+
+
+@pytest.mark.parametrize("M", [1, 15, 17, 63, 65, 100, 257, 1000])
+def test_any_m_equals_padded(cuda, hk, M):
+    """Unpadded call == reference-style pad + configured call + slice (bit-exact)."""
+    g = torch.Generator(device=cuda).manual_seed(M)
+    K, N = 512, 768
+    a = torch.randn(M, K, generator=g, device=cuda).half()
+    b = torch.randn(K, N, generator=g, device=cuda).to(torch.float8_e5m2)
+    bp = hk.prepack_b_for_scaled_mm(b)
+    s = torch.tensor(0.5, device=cuda)
+    bias = torch.randn(N, generator=g, device=cuda).half()
+    y = hk.scaled_mm_hip_any_m(a, bp, s, bias, torch.float16)
+    cfg = hk.any_m_config(M)
+    bm = 16 * cfg[0] * cfg[3]
+    mp = (M + bm - 1) // bm * bm
+    ap = torch.nn.functional.pad(a, (0, 0, 0, mp - M))
+    yp = hk.scaled_mm_hip_configured(ap, bp, s, bias, torch.float16, *cfg)[:M]
+    torch.cuda.synchronize()
+    assert torch.equal(y, yp)
