@@ -22,6 +22,7 @@
 //     (agent-scope) loads, stores and atomics; the splits of a strip are also
 //     placed on one XCD (workgroup p runs on XCD p % 8).
 #include "feather_common.h"
+#include "lds_dma.h"
 #include "scaled_mm_dispatch.h"
 
 namespace feather {
@@ -29,16 +30,25 @@ namespace {
 
 constexpr int kWaves = 16;
 
-template <int MT, int CT, bool kBf16, bool kE4m3>
+// Bytes of LDS A slab per wave and stage: MT row tiles of 16 rows x 128 bytes.
+constexpr int kSlabTile = 16 * 128;
+
+template <int MT, int CT, bool kLdsA, bool kBf16, bool kE4m3>
 __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
     int nstrips, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters) {
-    constexpr int U = (MT * 2 + CT) <= 4 ? 4 : 2;  // stages in flight per wave
+    // stages in flight per wave (within the 128 VGPRs a 16-wave workgroup allows)
+    constexpr int U = (MT * 2 + CT) <= 4 ? 4 : (MT * 2 + CT) < 10 ? 2 : 1;
     constexpr int kRows = MT * 16;
     constexpr int kCols = CT * 16;
     constexpr int kRedStride = kCols + 1;  // floats per reduction row (+1 pad)
-    __shared__ float red[kWaves][kRows][kRedStride];
+    constexpr int kRedBytes = kWaves * kRows * kRedStride * 4;
+    constexpr int kSlabBytes = kLdsA ? kWaves * U * MT * kSlabTile : 0;
+    static_assert(kRedBytes <= 160 * 1024 && kSlabBytes <= 160 * 1024, "LDS budget");
+    // the per-wave A slabs and the reduction buffer share one LDS block
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kRedBytes > kSlabBytes ? kRedBytes : kSlabBytes];
+    float(*red)[kRows][kRedStride] = reinterpret_cast<float(*)[kRows][kRedStride]>(smem);
     __shared__ int last_flag;
 
     // ---- workgroup -> (strip, K split); splits of a strip share an XCD ----
@@ -74,6 +84,34 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     for (int base = st_begin + wave; base < st_end; base += kWaves * U) {
         uint4 braw[U][CT];
         uint4 araw[U][MT][2];
+        if constexpr (kLdsA) {
+            // A through LDS: each copy instruction fetches 8 rows x 128 bytes
+            // (whole cache lines), which costs half the L1 lookups of loading
+            // the MFMA layout (16 rows x 2 separate 16-byte pieces) directly.
+            // Row r of a 16-row tile holds its 64-K stage as 8 chunks of 16
+            // bytes, chunk c at position c ^ swz(r). Each wave uses its own
+            // slab, so only this wave's copy count is waited for.
+            uint8_t* slab = smem + wave * (U * MT * kSlabTile);
+            if (base > st_begin + wave) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): last slab reads done
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int st = base + u * kWaves;
+                if (st < st_end) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const int r16 = 8 * j + (lane >> 3);
+                            const int row = mt * 16 + r16 < M ? mt * 16 + r16 : M - 1;
+                            int c = (lane & 7) ^ swz(r16);
+                            if (st * 4 + (c >> 1) >= kgroups) c = 0;  // past K: any in-row chunk (zeroed below)
+                            dma16(A, (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + st * 64 + c * 8) * 2u,
+                                  slab + (u * MT + mt) * kSlabTile + j * 1024);
+                        }
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int st = base + u * kWaves;
@@ -86,16 +124,36 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
                                   ? *reinterpret_cast<const uint4*>(Bp + (static_cast<int64_t>(kg) * N + col) * 16)
                                   : make_uint4(0u, 0u, 0u, 0u);
             }
+            if constexpr (!kLdsA) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int row = mt * 16 + lr;
-                if (kval && row < M) {
-                    const uint4* ap = reinterpret_cast<const uint4*>(A + static_cast<int64_t>(row) * K + kg * 16);
-                    araw[u][mt][0] = ap[0];
-                    araw[u][mt][1] = ap[1];
-                } else {
-                    araw[u][mt][0] = make_uint4(0u, 0u, 0u, 0u);
-                    araw[u][mt][1] = make_uint4(0u, 0u, 0u, 0u);
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int row = mt * 16 + lr;
+                    if (kval && row < M) {
+                        const uint4* ap = reinterpret_cast<const uint4*>(A + static_cast<int64_t>(row) * K + kg * 16);
+                        araw[u][mt][0] = ap[0];
+                        araw[u][mt][1] = ap[1];
+                    } else {
+                        araw[u][mt][0] = make_uint4(0u, 0u, 0u, 0u);
+                        araw[u][mt][1] = make_uint4(0u, 0u, 0u, 0u);
+                    }
+                }
+            }
+        }
+        if constexpr (kLdsA) {
+            wait_vmcnt<0>();
+            const uint8_t* slab = smem + wave * (U * MT * kSlabTile);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int st = base + u * kWaves;
+                const bool kval = st < st_end && st * 4 + lg < kgroups;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint4 v = *reinterpret_cast<const uint4*>(
+                            slab + (u * MT + mt) * kSlabTile + lr * 128 + (((2 * lg + h) ^ swz(lr)) << 4));
+                        araw[u][mt][h] = kval ? v : make_uint4(0u, 0u, 0u, 0u);
+                    }
                 }
             }
         }
@@ -116,6 +174,7 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
         }
     }
 
+    if constexpr (kLdsA) __syncthreads();  // the reduction buffer overlays other waves' slabs
     // accumulator element i of lane (lr, lg) is (row 4*lg + i, col lr) of its 16x16 tile
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -188,13 +247,13 @@ int ct_unsplit(int mt, int64_t N) {
     return 1;
 }
 
-template <int MT, int CT>
+template <int MT, int CT, bool LDSA = false>
 void launch_mt(const MmArgs& p, int ksplit, float* partials, uint32_t* counters, hipStream_t stream) {
     const int nstrips = static_cast<int>((p.N + 16 * CT - 1) / (16 * CT));
     const dim3 grid(static_cast<uint32_t>(nstrips * ksplit));
     const dim3 block(64 * kWaves);
 #define FEATHER_SMALLM_LAUNCH(BF, E4)                                                                       \
-    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, CT, BF, E4>), grid, block, 0, stream, p.a, p.b, p.scale, \
+    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, CT, LDSA, BF, E4>), grid, block, 0, stream, p.a, p.b, p.scale, \
                        p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),     \
                        p.has_scale, p.has_bias, nstrips, ksplit, partials, counters)
     if (p.out_bf16) {
@@ -254,9 +313,18 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
         }
     }
     const bool wide = ct_unsplit(mt, p.N) == 4;
+    // A through LDS needs every byte offset into A to fit the copy's 32-bit lane offset
+    const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
     switch (mt) {
-        case 1: wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream); return true;
-        case 2: wide ? launch_mt<2, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<2, 1>(p, 1, nullptr, nullptr, stream); return true;
+        case 1:
+            if (lds_a) wide ? launch_mt<1, 4, true>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1, true>(p, 1, nullptr, nullptr, stream);
+            else wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream);
+            return true;
+        case 2:  // (the 2 x 4 tile keeps direct A loads: its LDS variant runs out of VGPRs)
+            if (wide) launch_mt<2, 4>(p, 1, nullptr, nullptr, stream);
+            else if (lds_a) launch_mt<2, 1, true>(p, 1, nullptr, nullptr, stream);
+            else launch_mt<2, 1>(p, 1, nullptr, nullptr, stream);
+            return true;
         case 3: launch_mt<3, 1>(p, 1, nullptr, nullptr, stream); return true;
         case 4: launch_mt<4, 1>(p, 1, nullptr, nullptr, stream); return true;
         default: return false;
