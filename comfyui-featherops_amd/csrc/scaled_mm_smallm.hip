@@ -39,7 +39,9 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
     int nstrips, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters) {
     // stages in flight per wave (within the 128 VGPRs a 16-wave workgroup allows)
-    constexpr int U = (MT * 2 + CT) <= 4 ? 4 : (MT * 2 + CT) < 10 ? 2 : 1;
+    // and, with A through LDS, within 16 waves x U x MT x 2 KB of slabs
+    constexpr int U0 = (MT * 2 + CT) <= 4 ? 4 : (MT * 2 + CT) < 10 ? 2 : 1;
+    constexpr int U = kLdsA && U0 * MT > 4 ? 4 / MT : U0;
     constexpr int kRows = MT * 16;
     constexpr int kCols = CT * 16;
     constexpr int kRedStride = kCols + 1;  // floats per reduction row (+1 pad)
@@ -306,9 +308,16 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
         uint32_t* counters = static_cast<uint32_t*>(workspace);
         float* partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
                                                    (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256);
+        const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
         switch (mt) {
-            case 3: launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream); return true;
-            case 4: launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream); return true;
+            case 3:
+                if (lds_a) launch_mt<3, ct_split(3), true>(p, ks, partials, counters, stream);
+                else launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream);
+                return true;
+            case 4:
+                if (lds_a) launch_mt<4, ct_split(4), true>(p, ks, partials, counters, stream);
+                else launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream);
+                return true;
             default: return false;
         }
     }
