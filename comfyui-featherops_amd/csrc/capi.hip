@@ -77,6 +77,23 @@ int tuning_smallm_groups() {
     return g;
 }
 
+// M <= 64 runs on the small-M kernel or, for K % 64 == 0 and M > 48 (or
+// M > 32 with a weight larger than 4096 x 4096), on the LDS-DMA split-K tiles:
+// the small-M kernel re-reads the activations once per 16-32 columns, which
+// past 32 rows costs more than the tiles' shared LDS stages and split-K
+// reduction (measured on MI355X, weights rotated past the MALL: M=64
+// N=13824 K=5120 26 us vs 83 us; M=33..48 at N=K=4096 the small-M kernel is
+// 10-15% faster). FEATHEROPS_SMALLM_KERNEL (tuning knob): 0 = small-M kernel
+// for every M <= 64, 1 = split-K tiles for every M <= 64 with K % 64 == 0.
+bool use_lds_splitk(int64_t M, int64_t N, int64_t K) {
+    static const int v = [] {
+        const char* e = getenv("FEATHEROPS_SMALLM_KERNEL");
+        return e ? atoi(e) : -1;
+    }();
+    if (M > 64 || K % 64 != 0 || v == 0) return false;
+    return v == 1 || M > 48 || (M > 32 && N * K > int64_t(4096) * 4096);
+}
+
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
 }  // namespace
@@ -94,6 +111,7 @@ size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int blo
                                         int unroll_k, int repeat_m, int repeat_n) {
     const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
     if (kid != feather::kSmallM) return 0;
+    if (use_lds_splitk(M, N, K)) return feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).workspace_bytes;
     return feather::smallm_workspace_bytes(M, N, K, tuning_smallm_groups());
 }
 
@@ -122,7 +140,10 @@ bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, cons
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
     p.group_m = tuning_group_m();
     p.smallm_min_groups = tuning_smallm_groups();
-    if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
+    if (kid == feather::kSmallM) {
+        if (use_lds_splitk(M, N, K)) return feather::launch_lds_splitk(p, workspace, workspace_bytes, stream);
+        return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
+    }
     if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
 }

@@ -38,6 +38,13 @@ enum KernelId : int {
     kLds256x128 = 22,
     kLds128x256 = 23,
     kLds128x128 = 24,
+    // LDS-DMA tiles for M <= 64 with a K split across workgroups
+    kLdsSk64x64 = 30,
+    kLdsSk64x128 = 31,
+    kLdsSk64x256 = 32,
+    kLdsSk32x64 = 33,
+    kLdsSk32x128 = 34,
+    kLdsSk32x256 = 35,
 };
 
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
@@ -49,5 +56,16 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
 size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups);
 int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups);
 bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
+
+struct SplitKPlan {
+    int kernel_id;          // 0: not applicable
+    int ksplit;
+    int tiles;
+    size_t counter_bytes;   // arrival counters (zero between calls), 256-byte padded
+    size_t workspace_bytes; // counters + ksplit fp32 partial tiles per output tile
+};
+SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target);
+// Same workspace contract as launch_smallm_kernel.
+bool launch_lds_splitk(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace feather

@@ -44,7 +44,7 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool 
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
-    int tiles_m, int tiles_n, int group_m) {
+    int tiles_m, int tiles_n, int group_m, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters) {
     constexpr int kWaves = WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M;
     constexpr int WTN = BN / WAVES_N;
@@ -69,13 +69,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf2[kStage];
 
-    // ---- tile index: XCD-contiguous grouped raster ----
-    const int total = tiles_m * tiles_n;
+    // ---- tile index: XCD-contiguous grouped raster; the K splits of a tile
+    // are consecutive in that order (so mostly on one XCD) ----
+    const int total = tiles_m * tiles_n * ksplit;
     const int pid = blockIdx.x;
     const int xcd = pid % kNumXcd;
     const int per = total / kNumXcd;
     const int rem = total % kNumXcd;
-    const int lin = xcd * per + (xcd < rem ? xcd : rem) + pid / kNumXcd;
+    const int vlin = xcd * per + (xcd < rem ? xcd : rem) + pid / kNumXcd;
+    const int lin = vlin / ksplit;
+    const int q = vlin - lin * ksplit;
     const int group_size = group_m * tiles_n;
     const int gid = lin / group_size;
     const int first_m = gid * group_m;
@@ -93,7 +96,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const int wave_n = wave / WAVES_M;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int nk = K / kBK;
+    // K split q covers stages [kt0, kt0 + nk); the host picks ksplit so none is empty
+    const int nk_all = K / kBK;
+    const int per_split = (nk_all + ksplit - 1) / ksplit;
+    const int kt0 = q * per_split;
+    const int nk = (nk_all - kt0) < per_split ? (nk_all - kt0) : per_split;
 
     // ---- per-lane copy offsets (fixed), per-stage SGPR bases ----
     // A copy j of this wave fills rows r0..r0+7 of the tile, r0 = (j * kWaves + wave) * 8.
@@ -114,9 +121,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         const int lcol = (n0 + chunk % BN < N ? n0 + chunk % BN : N - 1) - n0;
         b_off[j] = static_cast<uint32_t>((kb * N + lcol) * 16);
     }
-    const uint8_t* a_base = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * K * 2;
-    const uint8_t* b_base = Bp + static_cast<int64_t>(n0) * 16;
     const int64_t b_stage_bytes = static_cast<int64_t>(N) * 64;  // 4 K groups of N x 16 bytes
+    const uint8_t* a_base = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * K * 2 + kt0 * (kBK * 2);
+    const uint8_t* b_base = Bp + static_cast<int64_t>(n0) * 16 + kt0 * b_stage_bytes;
 
     auto stage_buf = [&](auto tag) -> uint8_t* {
         constexpr int b = decltype(tag)::value;
@@ -269,9 +276,69 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         }
     }
 
+    const float s = has_scale ? scale[0] : 1.0f;
+    // (K split: only the 32- and 64-row tiles are ever launched with ksplit > 1)
+    if constexpr (BM <= 64) if (ksplit > 1) {
+        // ---- K split: each workgroup writes its fp32 accumulators to the
+        // workspace in fragment order (lane-contiguous 16-byte pieces) and
+        // bumps the tile's arrival counter; the workgroup that arrives last
+        // adds the ksplit partials in split order (deterministic), then runs
+        // the normal epilogue and re-zeroes the counter. Partial stores/loads
+        // are device-coherent (sc1) buffer accesses and the counter an
+        // agent-scope atomic; the vmcnt wait makes every partial store
+        // complete before the arrival count.
+        constexpr int kTileBytes = BM * BN * 4;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            partials + static_cast<int64_t>(lin) * ksplit * (kTileBytes / 4), 0, ksplit * kTileBytes, 0x00020000);
+        auto frag_off = [&](int rm, int rn) { return (((wave * RM + rm) * RN + rn) * 64 + lane) * 16; };
+        constexpr int kCoherent = 16;  // sc1
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+            for (int rn = 0; rn < RN; ++rn)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[rm][rn]), prs,
+                                                       q * kTileBytes + frag_off(rm, rn), 0, kCoherent);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __shared__ int last_flag;
+        __syncthreads();
+        if (tid == 0)
+            last_flag = __hip_atomic_fetch_add(&counters[lin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        static_cast<uint32_t>(ksplit - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        // the partials are re-read in split order, kQ splits' loads in flight at a time
+        constexpr int kQ = RM * RN <= 4 ? 4 : RM * RN <= 8 ? 2 : 1;
+#pragma unroll
+        for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q0 = 0; q0 < ksplit; q0 += kQ) {
+            f32x4 t[kQ][RM][RN];
+#pragma unroll
+            for (int j = 0; j < kQ; ++j)
+#pragma unroll
+                for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+                    for (int rn = 0; rn < RN; ++rn)
+                        t[j][rm][rn] = q0 + j < ksplit
+                                           ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                           prs, (q0 + j) * kTileBytes + frag_off(rm, rn),
+                                                                           0, kCoherent))
+                                           : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kQ; ++j)
+#pragma unroll
+                for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+                    for (int rn = 0; rn < RN; ++rn) acc[rm][rn] += t[j][rm][rn];
+        }
+        if (tid == 0)  // ready for the next call on this stream
+            __hip_atomic_store(&counters[lin], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // ---- epilogue (LDS reused after every wave is past its last stage) ----
     stage_barrier();
-    const float s = has_scale ? scale[0] : 1.0f;
     uint8_t* sc = sbuf0 + wave * kCWaveBytes;
     const int out_col0 = n0 + wave_n * WTN;
     constexpr int kChunksPerRow = WTN / 8;
@@ -306,16 +373,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int PIPE>
-void launch_lds(const MmArgs& p, hipStream_t stream) {
+void launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* partials = nullptr,
+                uint32_t* counters = nullptr) {
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
     const int group_m = p.group_m > 0 ? p.group_m : 4;
-    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n));
+    const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
 #define FEATHER_LDS_LAUNCH(BF, E4)                                                                                    \
     hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4>), grid, block, 0, stream, p.a,   \
                        p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),                      \
-                       static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m)
+                       static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, \
+                       partials, counters)
     if (p.out_bf16) {
         if (p.b_e4m3) FEATHER_LDS_LAUNCH(true, true);
         else FEATHER_LDS_LAUNCH(true, false);
@@ -327,27 +396,81 @@ void launch_lds(const MmArgs& p, hipStream_t stream) {
 }
 
 template <int PIPE>
-bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream) {
+bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks = 1, float* partials = nullptr,
+                     uint32_t* counters = nullptr) {
     switch (kernel_id) {
         case kLds256x256w2x4: launch_lds<256, 256, 2, 4, PIPE>(p, stream); return true;
         case kLds256x256w4x2: launch_lds<256, 256, 4, 2, PIPE>(p, stream); return true;
         case kLds256x128: launch_lds<256, 128, 4, 2, PIPE>(p, stream); return true;
         case kLds128x256: launch_lds<128, 256, 2, 4, PIPE>(p, stream); return true;
         case kLds128x128: launch_lds<128, 128, 2, 2, PIPE>(p, stream); return true;
+        case kLdsSk64x64: launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLdsSk64x128: launch_lds<64, 128, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLdsSk64x256: launch_lds<64, 256, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLdsSk32x64: launch_lds<32, 64, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLdsSk32x128: launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLdsSk32x256: launch_lds<32, 256, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
         default: return false;
     }
 }
 
 }  // namespace
 
-bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
-    if (p.K % kBK != 0) return false;
+int lds_pipe_env() {
     // FEATHEROPS_LDS_PIPE: 1 (default) = operand-prefetch schedule, 0 = plain schedule
     static const int pipe_env = [] {
         const char* e = getenv("FEATHEROPS_LDS_PIPE");
         return e ? atoi(e) : 1;
     }();
-    return pipe_env == 0 ? launch_lds_pipe<0>(kernel_id, p, stream) : launch_lds_pipe<1>(kernel_id, p, stream);
+    return pipe_env;
+}
+
+bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
+    if (p.K % kBK != 0) return false;
+    return lds_pipe_env() == 0 ? launch_lds_pipe<0>(kernel_id, p, stream) : launch_lds_pipe<1>(kernel_id, p, stream);
+}
+
+// Split-K plan for M <= 64: a 32- or 64-row tile and enough K splits to give
+// about `target` workgroups (each split keeps at least one 64-K stage).
+// Measured on MI355X (weights rotated past the MALL): 64 x 64 tiles beat
+// 64 x 128 / 64 x 256 at M = 64 for N = 3072..13824, and 32 x 128 is the best
+// 32-row tile (the small-M kernel still wins at M <= 32).
+SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
+    SplitKPlan pl{};
+    if (M <= 0 || M > 64 || K % kBK != 0) return pl;
+    const int bm = M <= 32 ? 32 : 64;
+    const int bn = bm == 32 ? 128 : 64;
+    const int64_t tiles = (N + bn - 1) / bn;
+    const int64_t nk = K / kBK;
+    int64_t ks = (target + tiles - 1) / tiles;
+    if (ks > nk) ks = nk;
+    if (ks > 32) ks = 32;
+    if (ks < 1) ks = 1;
+    const int64_t per = (nk + ks - 1) / ks;
+    ks = (nk + per - 1) / per;  // no empty split
+    pl.kernel_id = bm == 32 ? (bn == 64 ? kLdsSk32x64 : bn == 128 ? kLdsSk32x128 : kLdsSk32x256)
+                            : (bn == 64 ? kLdsSk64x64 : bn == 128 ? kLdsSk64x128 : kLdsSk64x256);
+    pl.ksplit = static_cast<int>(ks);
+    pl.tiles = static_cast<int>(tiles);
+    pl.counter_bytes = ks > 1 ? (static_cast<size_t>(tiles) * 4 + 255) / 256 * 256 : 0;
+    pl.workspace_bytes = ks > 1 ? pl.counter_bytes + static_cast<size_t>(tiles) * ks * bm * bn * 4 : 0;
+    return pl;
+}
+
+bool launch_lds_splitk(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int target = p.smallm_min_groups > 0 ? p.smallm_min_groups : 256;
+    const SplitKPlan pl = lds_splitk_plan(p.M, p.N, p.K, target);
+    if (pl.kernel_id == 0) return false;
+    int ks = pl.ksplit;
+    uint32_t* counters = nullptr;
+    float* partials = nullptr;
+    if (ks > 1 && (workspace == nullptr || workspace_bytes < pl.workspace_bytes)) ks = 1;
+    if (ks > 1) {
+        counters = static_cast<uint32_t*>(workspace);
+        partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + pl.counter_bytes);
+    }
+    return lds_pipe_env() == 0 ? launch_lds_pipe<0>(pl.kernel_id, p, stream, ks, partials, counters)
+                               : launch_lds_pipe<1>(pl.kernel_id, p, stream, ks, partials, counters);
 }
 
 }  // namespace feather

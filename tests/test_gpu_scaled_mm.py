@@ -203,6 +203,9 @@ def test_small_m_split_k_workspace(cuda, M, N, K):
         assert_gemm_close(c, ref, torch.float16, f"ws {M}x{N}x{K}")
         outs.append(c)
     assert torch.equal(outs[0], outs[1]), "split-K reduction must be deterministic"
-    if nbytes:  # split across workgroups (M > 32): 32-column strips, one counter each
-        strips = (N + 31) // 32
-        assert (ws[: strips * 4] == 0).all(), "arrival counters must be left at zero"
+    if nbytes:
+        # split across workgroups (M > 32): the workspace starts with one arrival
+        # counter per 64-column tile (LDS split-K path) or per 32-column strip
+        # (small-M kernel); the first (N + 63) // 64 are counters either way
+        tiles = (N + 63) // 64
+        assert (ws[: tiles * 4] == 0).all(), "arrival counters must be left at zero"
