@@ -24,7 +24,7 @@ constexpr Cfg kConfigs[] = {
     {1, 2, 2, 2, 2}, {1, 2, 4, 2, 2}, {2, 1, 2, 2, 2}, {2, 1, 4, 2, 2}, {1, 4, 2, 4, 2}, {1, 4, 4, 4, 2},
     {1, 8, 2, 8, 2}, {1, 8, 4, 8, 2}, {2, 2, 2, 4, 4}, {2, 2, 4, 4, 4}, {2, 4, 2, 4, 2}, {2, 4, 4, 4, 2},
     {2, 4, 2, 4, 4}, {2, 4, 4, 4, 4}, {4, 2, 2, 2, 4}, {4, 2, 4, 2, 4},
-    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4}, {4, 2, 4, 4, 8},
+    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4}, {4, 2, 4, 4, 8}, {2, 4, 4, 8, 3},
 };
 
 bool known_config(int wm, int wn, int u, int rm, int rn) {
@@ -40,6 +40,7 @@ int kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     const int bm = 16 * wm * rm;
     const int bn = 16 * wn * rn;
     const bool lds = K % 64 == 0;
+    if (bm >= 256 && bn == 192) return lds ? feather::kLds256x192 : feather::kTile256x128;
     if (bm >= 256 && bn >= 256) {
         if (!lds) return feather::kTile256x256;
         return wm > wn ? feather::kLds256x256w4x2 : feather::kLds256x256w2x4;

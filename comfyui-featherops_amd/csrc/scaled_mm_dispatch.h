@@ -38,6 +38,7 @@ enum KernelId : int {
     kLds256x128 = 22,
     kLds128x256 = 23,
     kLds128x128 = 24,
+    kLds256x192 = 25,
     // LDS-DMA tiles for M <= 64 with a K split across workgroups
     kLdsSk64x64 = 30,
     kLdsSk64x128 = 31,

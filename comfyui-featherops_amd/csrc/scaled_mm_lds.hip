@@ -56,9 +56,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     constexpr int kStage = kAStage + kBStage;
     constexpr int kAInst = kAStage / 1024;  // 1 KB wave copies per stage
     constexpr int kBInst = kBStage / 1024;
-    static_assert(kAInst % kWaves == 0 && kBInst % kWaves == 0, "copies must split evenly over waves");
+    static_assert(kAInst % kWaves == 0, "A copies must split evenly over waves");
     constexpr int kAPerWave = kAInst / kWaves;
-    constexpr int kBPerWave = kBInst / kWaves;
+    // B copies are rounded up to a whole number per wave; the surplus slots
+    // repeat the last copy (same bytes to the same LDS address), so every
+    // wave issues, and waits for, the same number of copies per stage.
+    constexpr int kBPerWave = (kBInst + kWaves - 1) / kWaves;
     constexpr int kLoadsPerStage = kAPerWave + kBPerWave;
     static_assert(BN % 64 == 0, "a B copy must stay inside one K group");
     constexpr int kCRowBytes = WTN * 2 + 16;
@@ -112,11 +115,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         const int lrow = (m0 + row < M ? m0 + row : M - 1) - m0;
         a_off[j] = static_cast<uint32_t>(lrow * K * 2 + c * 16);
     }
-    // B copy j covers chunks [base, base+64) of the (4 x BN) stage, base = (j*kWaves+wave)*64.
+    // B copy j covers chunks [base, base+64) of the (4 x BN) stage, base = b_copy(j) * 64.
+    auto b_copy = [&](int j) { return (j * kWaves + wave) < kBInst ? (j * kWaves + wave) : kBInst - 1; };
     uint32_t b_off[kBPerWave];
 #pragma unroll
     for (int j = 0; j < kBPerWave; ++j) {
-        const int chunk = (j * kWaves + wave) * 64 + lane;
+        const int chunk = b_copy(j) * 64 + lane;
         const int kb = chunk / BN;
         const int lcol = (n0 + chunk % BN < N ? n0 + chunk % BN : N - 1) - n0;
         b_off[j] = static_cast<uint32_t>((kb * N + lcol) * 16);
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             dma16(a_base + kt * (kBK * 2), a_off[i], sa + ((i * kWaves + wave) * 8) * 128);
         } else {
             const int j = i - kAPerWave;
-            dma16(b_base + kt * b_stage_bytes, b_off[j], sa + kAStage + ((j * kWaves + wave) * 64) * 16);
+            dma16(b_base + kt * b_stage_bytes, b_off[j], sa + kAStage + (b_copy(j) * 64) * 16);
         }
     };
     auto issue_stage = [&](auto tag, int kt) {
@@ -149,7 +153,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
         for (int j = 0; j < kAPerWave; ++j) dma16(ab, a_off[j], sa + ((j * kWaves + wave) * 8) * 128);
 #pragma unroll
-        for (int j = 0; j < kBPerWave; ++j) dma16(bb, b_off[j], sb + ((j * kWaves + wave) * 64) * 16);
+        for (int j = 0; j < kBPerWave; ++j) dma16(bb, b_off[j], sb + (b_copy(j) * 64) * 16);
     };
     // LDS byte offset of this lane's A operand for M repeat rm, K half kh
     auto a_lds = [&](int rm, int kh) -> int {
@@ -404,6 +408,7 @@ bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks 
         case kLds256x128: launch_lds<256, 128, 4, 2, PIPE>(p, stream); return true;
         case kLds128x256: launch_lds<128, 256, 2, 4, PIPE>(p, stream); return true;
         case kLds128x128: launch_lds<128, 128, 2, 2, PIPE>(p, stream); return true;
+        case kLds256x192: launch_lds<256, 192, 2, 4, PIPE>(p, stream); return true;
         case kLdsSk64x64: launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
         case kLdsSk64x128: launch_lds<64, 128, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
         case kLdsSk64x256: launch_lds<64, 256, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;

@@ -183,16 +183,17 @@ def _(a, b_prepacked, scale, bias, out_dtype, block_warps_m, block_warps_n, unro
 
 scaled_mm_hip_configured = _configured_op
 
-# Reference configurations (hip_kernel.py:60-89), then three gfx950 tiles:
-# (2,4,4,8,4) -> 256x256 (2x4 waves), (4,2,4,4,8) -> 256x256 (4x2 waves) and
-# (4,2,4,4,4) -> 256x128 output tiles.
+# Reference configurations (hip_kernel.py:60-89), then four gfx950 tiles:
+# (2,4,4,8,4) -> 256x256 (2x4 waves), (4,2,4,4,8) -> 256x256 (4x2 waves),
+# (4,2,4,4,4) -> 256x128 and (2,4,4,8,3) -> 256x192 output tiles (the last one
+# gives M=4096, N=3072 exactly 256 tiles, one per CU).
 _CONFIGS = [
     (1, 1, 2, 1, 2), (1, 1, 4, 1, 2), (1, 2, 2, 1, 2), (1, 2, 4, 1, 2), (1, 4, 2, 1, 2), (1, 4, 4, 1, 2),
     (1, 8, 2, 1, 2), (1, 8, 4, 1, 2), (1, 1, 2, 2, 2), (1, 1, 4, 2, 2), (1, 1, 2, 4, 4), (1, 1, 4, 4, 4),
     (1, 2, 2, 2, 2), (1, 2, 4, 2, 2), (2, 1, 2, 2, 2), (2, 1, 4, 2, 2), (1, 4, 2, 4, 2), (1, 4, 4, 4, 2),
     (1, 8, 2, 8, 2), (1, 8, 4, 8, 2), (2, 2, 2, 4, 4), (2, 2, 4, 4, 4), (2, 4, 2, 4, 2), (2, 4, 4, 4, 2),
     (2, 4, 2, 4, 4), (2, 4, 4, 4, 4), (4, 2, 2, 2, 4), (4, 2, 4, 2, 4),
-    (2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4),
+    (2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3),
 ]
 _CONFIGS = sorted(_CONFIGS, key=lambda x: (x[0], x[1], x[3], x[4], x[2]))
 

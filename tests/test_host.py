@@ -56,8 +56,10 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 23  # BlockM 128, BlockN 256
     assert hk.kernel_id(4096, 4096, 4096, (3, 3, 3, 3, 3)) == 0
     assert hk.kernel_id(4096, 4096, 4090, (2, 4, 4, 8, 4)) == 0  # K % 16 != 0
+    assert hk.kernel_id(4096, 3072, 3072, (2, 4, 4, 8, 3)) == 25  # 256x192
+    assert hk.kernel_id(4096, 3072, 3080, (2, 4, 4, 8, 3)) == 0  # K % 16 != 0
     for cfg in hk._CONFIGS:
-        assert hk.kernel_id(1024, 1024, 1024, cfg) in (5, 6, 20, 21, 22, 23, 24)
+        assert hk.kernel_id(1024, 1024, 1024, cfg) in (5, 6, 20, 21, 22, 23, 24, 25)
 
 
 def test_configs_keep_reference_entries(hk):
