@@ -108,29 +108,75 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 
 // amax of |x| (load path: x = w * ckpt_scale) as fp32 bits; NaN bit patterns
 // compare above +inf, so a NaN anywhere yields a NaN amax as torch.amax does.
+//
+// The maximum is taken over the weight's own bit patterns with the sign
+// cleared (for fp16, bf16 and fp32 alike that integer order is the order of
+// |x|, NaNs above +inf) and scaled by |ckpt_scale| once per workgroup:
+// rounding x * c is monotonic in |x| for a finite c, so max |fl(x c)| =
+// fl(max|x| * |c|). A non-finite checkpoint scale (where 0 * inf = NaN
+// breaks that) takes the per-element path.
+template <int DT>
+__device__ __forceinline__ uint32_t abs_max_words(uint4 t, uint32_t m) {
+    const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        if constexpr (DT == kDtypeF32) {
+            const uint32_t b = w[h] & 0x7fffffffu;
+            m = b > m ? b : m;
+        } else {
+            const uint32_t lo = w[h] & 0x7fffu, hi = (w[h] >> 16) & 0x7fffu;
+            m = lo > m ? lo : m;
+            m = hi > m ? hi : m;
+        }
+    }
+    return m;
+}
+
+template <int DT>
+__device__ __forceinline__ float abs_bits_to_f32(uint32_t m) {
+    if constexpr (DT == kDtypeF16) return half_bits_to_f32(static_cast<uint16_t>(m));
+    else if constexpr (DT == kDtypeBF16) return bf16_bits_to_f32(static_cast<uint16_t>(m));
+    else return bits_f32(m);
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ w, int64_t n,
                                                    const float* __restrict__ ckpt_scale, int premul,
                                                    uint32_t* __restrict__ amax_bits) {
     __shared__ uint32_t part[4];
     const float cs = (premul && ckpt_scale) ? ckpt_scale[0] : 1.0f;
+    const bool per_element = premul && !(__builtin_fabsf(cs) <= 3.402823466e38f);  // inf or NaN scale
     uint32_t m = 0u;
-    const int64_t ngroups = n / 16;
+    constexpr int kPerVec = DT == kDtypeF32 ? 4 : 8;  // elements per 16 bytes
+    const int64_t nvec = n / kPerVec;
+    const uint4* v16 = static_cast<const uint4*>(w);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
-        float v[16];
-        load16<DT>(w, g * 16, v);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t b = f32_bits(premul ? v[j] * cs : v[j]) & 0x7fffffffu;
+    if (!per_element) {
+        // native-bit maximum, four 16-byte loads in flight per thread
+        int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+        for (; i + 3 * stride < nvec; i += 4 * stride) {
+            const uint4 t0 = v16[i], t1 = v16[i + stride], t2 = v16[i + 2 * stride], t3 = v16[i + 3 * stride];
+            m = abs_max_words<DT>(t0, m);
+            m = abs_max_words<DT>(t1, m);
+            m = abs_max_words<DT>(t2, m);
+            m = abs_max_words<DT>(t3, m);
+        }
+        for (; i < nvec; i += stride) m = abs_max_words<DT>(v16[i], m);
+        if (blockIdx.x == 0 && threadIdx.x < n - nvec * kPerVec) {
+            const int64_t t = nvec * kPerVec + threadIdx.x;
+            const uint32_t b = DT == kDtypeF32 ? (static_cast<const uint32_t*>(w)[t] & 0x7fffffffu)
+                                               : (static_cast<const uint16_t*>(w)[t] & 0x7fffu);
             m = b > m ? b : m;
         }
-    }
-    // tail (n % 16 elements) handled by the first threads of block 0
-    if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
-        const float x = WeightType<DT>::load(w, ngroups * 16 + threadIdx.x);
-        const uint32_t b = f32_bits(premul ? x * cs : x) & 0x7fffffffu;
-        m = b > m ? b : m;
+        // to |x| as fp32 (exact), then the one multiply by |ckpt_scale|
+        float a = abs_bits_to_f32<DT>(m);
+        if (premul) a = a * __builtin_fabsf(cs);
+        m = f32_bits(a) & 0x7fffffffu;
+    } else {
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+            const uint32_t b = f32_bits(WeightType<DT>::load(w, i) * cs) & 0x7fffffffu;
+            m = b > m ? b : m;
+        }
     }
     m = wave_max_u32(m);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
@@ -318,7 +364,7 @@ void launch_quant(const QuantArgs& q, hipStream_t stream) {
     const bool premul = !q.native;
     if (!q.scale_in) {
         hipLaunchKernelGGL(zero_word_kernel, dim3(1), dim3(1), 0, stream, q.workspace);
-        hipLaunchKernelGGL((amax_kernel<DT>), dim3(grid_for(n / 16, 256, 4096)), dim3(256), 0, stream, q.w, n,
+        hipLaunchKernelGGL((amax_kernel<DT>), dim3(grid_for(n / 32, 256, 2048)), dim3(256), 0, stream, q.w, n,
                            q.ckpt_scale, premul ? 1 : 0, q.workspace);
     }
     const dim3 grid(static_cast<uint32_t>((q.K / 16 + 3) / 4), static_cast<uint32_t>((q.N + 63) / 64));
