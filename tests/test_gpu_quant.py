@@ -94,6 +94,24 @@ def test_load_path_with_checkpoint_scale(cuda, quant, dtype):
     assert np.array_equal(_bytes(qdata), O.prepack_transpose(codes))
 
 
+@pytest.mark.parametrize("ck", [-0.73, 0.0, float("inf"), 1e-30, 1.0e38])
+def test_load_path_checkpoint_scale_edge_values(cuda, quant, ck):
+    """amax is max|w| times |ckpt_scale| once per workgroup for a finite scale and
+    per element otherwise; both must equal amax(|float32(w) * ckpt_scale|)."""
+    g = torch.Generator().manual_seed(5)
+    w = (torch.randn(128, 256, generator=g) * 0.5).half()
+    w[0, :7] = 0.0  # zeros make inf * 0 = NaN for an infinite scale
+    qt = quant.make_feather_quantized_weight(w.to(cuda), torch.tensor(ck).to(cuda), torch.float16)
+    qdata, scale = quant.get_feather_plain_tensors(qt)
+    codes, s_ref = O.quantize_load(w.float().numpy(), O.DT_F32, ckpt_scale=np.float32(ck))
+    s_gpu = np.float32(scale.item())
+    if np.isnan(s_ref):
+        assert np.isnan(s_gpu)
+    else:
+        assert s_gpu == s_ref
+        assert np.array_equal(_bytes(qdata), O.prepack_transpose(codes))
+
+
 def test_special_inputs(cuda, quant):
     z = torch.zeros(32, 64, dtype=torch.float16, device=cuda)
     q, s = quant.quantize_fp8e5m2_scaled(z)
