@@ -35,7 +35,9 @@ bool known_config(int wm, int wn, int u, int rm, int rn) {
 
 // The tuple picks the output tile (BlockM x BlockN, capped at 256); the
 // LDS-DMA pipeline serves K % 64 == 0, the register-staged tile the rest.
-int kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
+// Shapes too small to fill the GPU with those tiles are routed first (see
+// splitk_route).
+int tile_kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     if (M <= 64) return feather::kSmallM;
     const int bm = 16 * wm * rm;
     const int bn = 16 * wn * rn;
@@ -78,22 +80,36 @@ int tuning_smallm_groups() {
     return g;
 }
 
-// M <= 64 runs on the small-M kernel or, for K % 64 == 0 and M > 48 (or
-// M > 32 with a weight larger than 4096 x 4096), on the LDS-DMA split-K tiles:
-// the small-M kernel re-reads the activations once per 16-32 columns, which
-// past 32 rows costs more than the tiles' shared LDS stages and split-K
-// reduction (measured on MI355X, weights rotated past the MALL: M=64
-// N=13824 K=5120 26 us vs 83 us; M=33..48 at N=K=4096 the small-M kernel is
-// 10-15% faster). FEATHEROPS_SMALLM_KERNEL (tuning knob): 0 = small-M kernel
-// for every M <= 64, 1 = split-K tiles for every M <= 64 with K % 64 == 0.
-bool use_lds_splitk(int64_t M, int64_t N, int64_t K) {
-    static const int v = [] {
-        const char* e = getenv("FEATHEROPS_SMALLM_KERNEL");
-        return e ? atoi(e) : -1;
-    }();
-    if (M > 64 || K % 64 != 0 || v == 0) return false;
-    return v == 1 || M > 48 || (M > 32 && N * K > int64_t(4096) * 4096);
+// Split-K LDS tiles (64 x 64, or 32 x 128 for M <= 32) with about 256
+// workgroups, for K % 64 == 0 and
+//   * 32 < M <= 64: M > 48, or a weight larger than 4096 x 4096 (the small-M
+//     kernel re-reads the activations once per 16-32 columns, which past 32
+//     rows costs more than shared LDS stages plus the split-K reduction;
+//     M=64 N=13824 K=5120: 26 us vs 83 us, while at M=33..48, N=K=4096 the
+//     small-M kernel is 10-15% faster);
+//   * M > 64 when 128 x 128 tiles would not fill the 256 CUs
+//     (ceil(M/128) * ceil(N/128) < 256): M=256 N=K=3072 15 us vs 28 us for the
+//     best tuple tile, M=1024 N=K=1024 8 us vs 11 us; from 256 such tiles on
+//     the tuple's tile wins (M=2048 N=K=3072: 46 us vs 60 us).
+// Measured on MI355X with the C++ bench. FEATHEROPS_SPLITK (tuning knob, read
+// on every call so that tests can reach the tuple's tile kernels at small
+// shapes): 0 = never, 1 = always (K % 64 == 0).
+int splitk_route(int64_t M, int64_t N, int64_t K) {
+    const char* e = getenv("FEATHEROPS_SPLITK");
+    const int v = e ? atoi(e) : -1;
+    if (K % 64 != 0 || v == 0) return feather::kKernelNone;
+    bool use = v == 1;
+    if (!use && M <= 64) use = M > 48 || (M > 32 && N * K > int64_t(4096) * 4096);
+    if (!use && M > 64) use = ((M + 127) / 128) * ((N + 127) / 128) < 256;
+    return use ? feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).kernel_id : feather::kKernelNone;
 }
+
+int kernel_for(int64_t M, int64_t N, int64_t K, int wm, int wn, int rm, int rn) {
+    const int sk = splitk_route(M, N, K);
+    return sk != feather::kKernelNone ? sk : tile_kernel_for(M, K, wm, wn, rm, rn);
+}
+
+bool is_splitk(int kid) { return kid >= feather::kLdsSk64x64 && kid <= feather::kLdsSk32x256; }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
@@ -105,14 +121,15 @@ int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps
                                 int repeat_m, int repeat_n) {
     if (!known_config(block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n)) return feather::kKernelNone;
     if (!sizes_ok(M, N, K)) return feather::kKernelNone;
-    return kernel_for(M, K, block_warps_m, block_warps_n, repeat_m, repeat_n);
+    return kernel_for(M, N, K, block_warps_m, block_warps_n, repeat_m, repeat_n);
 }
 
 size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
                                         int unroll_k, int repeat_m, int repeat_n) {
     const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    if (kid == feather::kKernelNone) return 0;
+    if (is_splitk(kid)) return feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).workspace_bytes;
     if (kid != feather::kSmallM) return 0;
-    if (use_lds_splitk(M, N, K)) return feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).workspace_bytes;
     return feather::smallm_workspace_bytes(M, N, K, tuning_smallm_groups());
 }
 
@@ -141,10 +158,8 @@ bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, cons
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
     p.group_m = tuning_group_m();
     p.smallm_min_groups = tuning_smallm_groups();
-    if (kid == feather::kSmallM) {
-        if (use_lds_splitk(M, N, K)) return feather::launch_lds_splitk(p, workspace, workspace_bytes, stream);
-        return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
-    }
+    if (is_splitk(kid)) return feather::launch_lds_splitk(p, workspace, workspace_bytes, stream);
+    if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
     if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
 }

@@ -442,10 +442,10 @@ bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
 // 32-row tile (the small-M kernel still wins at M <= 32).
 SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     SplitKPlan pl{};
-    if (M <= 0 || M > 64 || K % kBK != 0) return pl;
+    if (M <= 0 || K % kBK != 0) return pl;
     const int bm = M <= 32 ? 32 : 64;
     const int bn = bm == 32 ? 128 : 64;
-    const int64_t tiles = (N + bn - 1) / bn;
+    const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
     const int64_t nk = K / kBK;
     int64_t ks = (target + tiles - 1) / tiles;
     if (ks > nk) ks = nk;

@@ -41,7 +41,12 @@ def test_golden_small_all_kernels(cuda, hk):
                                    (256, 256, 512), (512, 256, 256), (100, 384, 320), (300, 512, 1040),
                                    (1024, 1024, 1024)])
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
-def test_shapes_and_tiles(cuda, M, N, K, out_dtype):
+@pytest.mark.parametrize("splitk", ["default", "0"])
+def test_shapes_and_tiles(cuda, monkeypatch, M, N, K, out_dtype, splitk):
+    """Every tile config on each shape; FEATHEROPS_SPLITK=0 keeps small shapes on
+    the tuple's tile kernel instead of the split-K tiles they are routed to."""
+    if splitk != "default":
+        monkeypatch.setenv("FEATHEROPS_SPLITK", splitk)
     g = torch.Generator().manual_seed(M * 7 + N + K)
     a = torch.randn(M, K, generator=g).half()
     packed, s = weight_like(N, K, g)

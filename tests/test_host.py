@@ -52,14 +52,21 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(32768, 13824, 5120, (4, 2, 4, 4, 8)) == 21  # same tile, 4x2 waves
     assert hk.kernel_id(32768, 13824, 5136, (2, 4, 4, 8, 4)) == 1  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(16, 4096, 4096, (1, 1, 2, 1, 2)) == 10  # small-M
-    assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(40, 4096, 4096, (1, 8, 4, 8, 2)) == 10
+    # split-K LDS tiles: 32 < M <= 64 (here M > 48), and shapes 128x128 tiles cannot spread over 256 CUs
+    assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 30
+    assert hk.kernel_id(40, 13824, 5120, (1, 1, 2, 1, 2)) == 30
+    assert hk.kernel_id(256, 3072, 3072, (2, 4, 4, 8, 4)) == 30
+    assert hk.kernel_id(2048, 3072, 3072, (2, 2, 4, 4, 4)) == 24
+    assert hk.kernel_id(256, 3072, 3088, (2, 2, 4, 4, 4)) == 4  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 23  # BlockM 128, BlockN 256
     assert hk.kernel_id(4096, 4096, 4096, (3, 3, 3, 3, 3)) == 0
     assert hk.kernel_id(4096, 4096, 4090, (2, 4, 4, 8, 4)) == 0  # K % 16 != 0
     assert hk.kernel_id(4096, 3072, 3072, (2, 4, 4, 8, 3)) == 25  # 256x192
     assert hk.kernel_id(4096, 3072, 3080, (2, 4, 4, 8, 3)) == 0  # K % 16 != 0
     for cfg in hk._CONFIGS:
-        assert hk.kernel_id(1024, 1024, 1024, cfg) in (5, 6, 20, 21, 22, 23, 24, 25)
+        assert hk.kernel_id(4096, 4096, 4096, cfg) in (5, 6, 20, 21, 22, 23, 24, 25)
+        assert hk.kernel_id(1024, 1024, 1024, cfg) == 30
 
 
 def test_configs_keep_reference_entries(hk):
