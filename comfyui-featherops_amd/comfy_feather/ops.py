@@ -147,7 +147,11 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
 
             def _forward_padded(self, x):
                 dtype_orig = x.dtype
-                x = x.contiguous().to(torch.float16)
+                x = x.contiguous()
+                if self.pad_m or x.dtype != torch.bfloat16:
+                    # (bf16 activations go to the any-M entry as they are: the
+                    # kernel rounds them to fp16 itself, the same values as this cast)
+                    x = x.to(torch.float16)
                 # no low-VRAM weight patches on the prepacked weight while casting
                 saved_weight_function = self.weight_function
                 self.weight_function = []

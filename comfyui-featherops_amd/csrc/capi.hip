@@ -109,7 +109,7 @@ int kernel_for(int64_t M, int64_t N, int64_t K, int wm, int wn, int rm, int rn) 
     return sk != feather::kKernelNone ? sk : tile_kernel_for(M, K, wm, wn, rm, rn);
 }
 
-bool is_splitk(int kid) { return kid >= feather::kLdsSk64x64 && kid <= feather::kLdsSk32x256; }
+bool is_splitk(int kid) { return kid == feather::kLdsSk64x64 || kid == feather::kLdsSk32x128; }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
@@ -133,13 +133,14 @@ size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int blo
     return feather::smallm_workspace_bytes(M, N, K, tuning_smallm_groups());
 }
 
-bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
-                                 uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
-                                 int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
-                                 int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
+bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_prepacked, const float* scale,
+                                 const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale,
+                                 int has_bias, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m,
+                                 int repeat_n, int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream) {
     const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
     if (kid == feather::kKernelNone) return false;
+    if (a_dtype != FEATHER_DTYPE_F16 && a_dtype != FEATHER_DTYPE_BF16) return false;
     if (b_dtype != FEATHER_B_E4M3FN && b_dtype != FEATHER_B_E5M2) return false;
     if (output_dtype != 0 && output_dtype != 1) return false;
     if (M == 0) return true;
@@ -156,12 +157,23 @@ bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, cons
     p.has_bias = has_bias ? 1 : 0;
     p.out_bf16 = output_dtype == 1;
     p.b_e4m3 = b_dtype == FEATHER_B_E4M3FN;
+    p.a_bf16 = a_dtype == FEATHER_DTYPE_BF16;
     p.group_m = tuning_group_m();
     p.smallm_min_groups = tuning_smallm_groups();
     if (is_splitk(kid)) return feather::launch_lds_splitk(p, workspace, workspace_bytes, stream);
     if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
     if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
+}
+
+bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                                 uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                                 int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                 int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+    return feather_launch_scaled_mm_ex(a, FEATHER_DTYPE_F16, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias,
+                                       block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
+                                       output_dtype, workspace, workspace_bytes, stream);
 }
 
 bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,

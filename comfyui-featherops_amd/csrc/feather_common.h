@@ -100,6 +100,29 @@ __device__ __forceinline__ void add_bias8(uint4& v, const uint16_t* bias) {
 
 __device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
+// An A-operand fragment of 8 activations: fp16 as stored, or bf16 converted
+// to fp16 with round-to-nearest-even (overflow -> +-inf, subnormals kept), the
+// same values as torch's x.to(float16) that the reference's Linear applies
+// before the GEMM (comfy_feather/ops.py:88). bf16 -> fp32 is exact (a shift);
+// v_cvt_pk_f16_f32 rounds two fp32 values to fp16 at once.
+template <bool kABf16>
+__device__ __forceinline__ half8_t a_frag(uint4 v) {
+    if constexpr (!kABf16) {
+        return as_half8(v);
+    } else {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x2 f = {bits_f32(w[i] << 16), bits_f32(w[i] & 0xffff0000u)};
+            o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+        }
+        return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+}
+
 // D(16x16,f32) += A(16x32,f16) * B(32x16,f16). Lane l supplies A row l%16 and
 // B column l%16 with 8 consecutive K slots each; lanes l and l+16*g share the
 // row/column and cover slot groups g = 0..3. Any K order that is the same for

@@ -8,7 +8,7 @@
 namespace feather {
 
 struct MmArgs {
-    const uint16_t* a;       // (M, K) fp16, row-major
+    const uint16_t* a;       // (M, K) fp16 (or bf16 when a_bf16), row-major
     const uint8_t* b;        // (K/16, N, 16) fp8 bytes
     const float* scale;      // device scalar, read when has_scale
     const uint16_t* bias;    // (N,) in the output type, read when has_bias
@@ -17,6 +17,7 @@ struct MmArgs {
     int has_scale, has_bias;
     bool out_bf16;
     bool b_e4m3;
+    bool a_bf16;             // activations are bf16 (converted to fp16 in the kernel; e5m2 weights only)
     int group_m;             // tile raster group height (0 = default)
     int smallm_min_groups;   // small-M: workgroup count the K split aims for (0 = default)
 };
@@ -39,15 +40,14 @@ enum KernelId : int {
     kLds128x256 = 23,
     kLds128x128 = 24,
     kLds256x192 = 25,
-    // LDS-DMA tiles for M <= 64 with a K split across workgroups
+    // LDS-DMA tiles with a K split across workgroups (small shapes)
     kLdsSk64x64 = 30,
-    kLdsSk64x128 = 31,
-    kLdsSk64x256 = 32,
-    kLdsSk32x64 = 33,
     kLdsSk32x128 = 34,
-    kLdsSk32x256 = 35,
 };
 
+// Every launcher returns false, and launches nothing, for a variant it does not
+// have (bf16 activations are served by the LDS-DMA and small-M kernels with
+// e5m2 weights only).
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
 // Small-M kernel. With a workspace of at least smallm_workspace_bytes() it
 // also splits K across workgroups; without one it splits K inside each

@@ -40,7 +40,7 @@ namespace {
 constexpr int kBK = 64;
 
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, bool kABf16>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
         for (int rm = 0; rm < RM; ++rm) {
             hook(rm);
-            const half8_t a = as_half8(araw[rm]);
+            const half8_t a = a_frag<kABf16>(araw[rm]);
 #pragma unroll
             for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a, bq[rn], acc[rm][rn]);
         }
@@ -377,44 +377,55 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int PIPE>
-void launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* partials = nullptr,
+bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* partials = nullptr,
                 uint32_t* counters = nullptr) {
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
     const int group_m = p.group_m > 0 ? p.group_m : 4;
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
-#define FEATHER_LDS_LAUNCH(BF, E4)                                                                                    \
-    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4>), grid, block, 0, stream, p.a,   \
-                       p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),                      \
-                       static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, \
-                       partials, counters)
+#define FEATHER_LDS_LAUNCH(BF, E4, AB)                                                                                \
+    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, AB>), grid, block, 0, stream,    \
+                       p.a, p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),                  \
+                       static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, partials,   \
+                       counters)
+    if (p.a_bf16) {
+        // bf16 activations: the small split-K tiles only (default schedule, e5m2
+        // weights). On the large tiles, where every A fragment is read by 2-4
+        // waves, converting each read costs more than a separate cast pass
+        // (measured at M=32768 N=13824 K=5120: 4.44 ms vs 3.68 ms cast + GEMM),
+        // so the caller converts A for them.
+        if constexpr (PIPE == 1 && BM <= 64) {
+            if (p.b_e4m3) return false;
+            if (p.out_bf16) FEATHER_LDS_LAUNCH(true, false, true);
+            else FEATHER_LDS_LAUNCH(false, false, true);
+            return true;
+        }
+        return false;
+    }
     if (p.out_bf16) {
-        if (p.b_e4m3) FEATHER_LDS_LAUNCH(true, true);
-        else FEATHER_LDS_LAUNCH(true, false);
+        if (p.b_e4m3) FEATHER_LDS_LAUNCH(true, true, false);
+        else FEATHER_LDS_LAUNCH(true, false, false);
     } else {
-        if (p.b_e4m3) FEATHER_LDS_LAUNCH(false, true);
-        else FEATHER_LDS_LAUNCH(false, false);
+        if (p.b_e4m3) FEATHER_LDS_LAUNCH(false, true, false);
+        else FEATHER_LDS_LAUNCH(false, false, false);
     }
 #undef FEATHER_LDS_LAUNCH
+    return true;
 }
 
 template <int PIPE>
 bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks = 1, float* partials = nullptr,
                      uint32_t* counters = nullptr) {
     switch (kernel_id) {
-        case kLds256x256w2x4: launch_lds<256, 256, 2, 4, PIPE>(p, stream); return true;
-        case kLds256x256w4x2: launch_lds<256, 256, 4, 2, PIPE>(p, stream); return true;
-        case kLds256x128: launch_lds<256, 128, 4, 2, PIPE>(p, stream); return true;
-        case kLds128x256: launch_lds<128, 256, 2, 4, PIPE>(p, stream); return true;
-        case kLds128x128: launch_lds<128, 128, 2, 2, PIPE>(p, stream); return true;
-        case kLds256x192: launch_lds<256, 192, 2, 4, PIPE>(p, stream); return true;
-        case kLdsSk64x64: launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
-        case kLdsSk64x128: launch_lds<64, 128, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
-        case kLdsSk64x256: launch_lds<64, 256, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
-        case kLdsSk32x64: launch_lds<32, 64, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
-        case kLdsSk32x128: launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
-        case kLdsSk32x256: launch_lds<32, 256, 1, 4, PIPE>(p, stream, ks, partials, counters); return true;
+        case kLds256x256w2x4: return launch_lds<256, 256, 2, 4, PIPE>(p, stream);
+        case kLds256x256w4x2: return launch_lds<256, 256, 4, 2, PIPE>(p, stream);
+        case kLds256x128: return launch_lds<256, 128, 4, 2, PIPE>(p, stream);
+        case kLds128x256: return launch_lds<128, 256, 2, 4, PIPE>(p, stream);
+        case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
+        case kLds256x192: return launch_lds<256, 192, 2, 4, PIPE>(p, stream);
+        case kLdsSk64x64: return launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters);
+        case kLdsSk32x128: return launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
         default: return false;
     }
 }
@@ -432,7 +443,8 @@ int lds_pipe_env() {
 
 bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
     if (p.K % kBK != 0) return false;
-    return lds_pipe_env() == 0 ? launch_lds_pipe<0>(kernel_id, p, stream) : launch_lds_pipe<1>(kernel_id, p, stream);
+    return lds_pipe_env() == 0 && !p.a_bf16 ? launch_lds_pipe<0>(kernel_id, p, stream)
+                                            : launch_lds_pipe<1>(kernel_id, p, stream);
 }
 
 // Split-K plan for M <= 64: a 32- or 64-row tile and enough K splits to give
@@ -453,8 +465,7 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     if (ks < 1) ks = 1;
     const int64_t per = (nk + ks - 1) / ks;
     ks = (nk + per - 1) / per;  // no empty split
-    pl.kernel_id = bm == 32 ? (bn == 64 ? kLdsSk32x64 : bn == 128 ? kLdsSk32x128 : kLdsSk32x256)
-                            : (bn == 64 ? kLdsSk64x64 : bn == 128 ? kLdsSk64x128 : kLdsSk64x256);
+    pl.kernel_id = bm == 32 ? kLdsSk32x128 : kLdsSk64x64;
     pl.ksplit = static_cast<int>(ks);
     pl.tiles = static_cast<int>(tiles);
     pl.counter_bytes = ks > 1 ? (static_cast<size_t>(tiles) * 4 + 255) / 256 * 256 : 0;
@@ -474,8 +485,8 @@ bool launch_lds_splitk(const MmArgs& p, void* workspace, size_t workspace_bytes,
         counters = static_cast<uint32_t*>(workspace);
         partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + pl.counter_bytes);
     }
-    return lds_pipe_env() == 0 ? launch_lds_pipe<0>(pl.kernel_id, p, stream, ks, partials, counters)
-                               : launch_lds_pipe<1>(pl.kernel_id, p, stream, ks, partials, counters);
+    return lds_pipe_env() == 0 && !p.a_bf16 ? launch_lds_pipe<0>(pl.kernel_id, p, stream, ks, partials, counters)
+                                            : launch_lds_pipe<1>(pl.kernel_id, p, stream, ks, partials, counters);
 }
 
 }  // namespace feather

@@ -33,7 +33,7 @@ constexpr int kWaves = 16;
 // Bytes of LDS A slab per wave and stage: MT row tiles of 16 rows x 128 bytes.
 constexpr int kSlabTile = 16 * 128;
 
-template <int MT, int CT, bool kLdsA, bool kBf16, bool kE4m3>
+template <int MT, int CT, bool kLdsA, bool kBf16, bool kE4m3, bool kABf16>
 __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
@@ -168,8 +168,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
                     const half8_t b1 = widen_fp8x8<kE4m3>(braw[u][ct].z, braw[u][ct].w);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
-                        acc[mt][ct] = mfma16x16x32(as_half8(araw[u][mt][0]), b0, acc[mt][ct]);
-                        acc[mt][ct] = mfma16x16x32(as_half8(araw[u][mt][1]), b1, acc[mt][ct]);
+                        acc[mt][ct] = mfma16x16x32(a_frag<kABf16>(araw[u][mt][0]), b0, acc[mt][ct]);
+                        acc[mt][ct] = mfma16x16x32(a_frag<kABf16>(araw[u][mt][1]), b1, acc[mt][ct]);
                     }
                 }
             }
@@ -250,22 +250,33 @@ int ct_unsplit(int mt, int64_t N) {
 }
 
 template <int MT, int CT, bool LDSA = false>
-void launch_mt(const MmArgs& p, int ksplit, float* partials, uint32_t* counters, hipStream_t stream) {
+bool launch_mt(const MmArgs& p, int ksplit, float* partials, uint32_t* counters, hipStream_t stream) {
     const int nstrips = static_cast<int>((p.N + 16 * CT - 1) / (16 * CT));
     const dim3 grid(static_cast<uint32_t>(nstrips * ksplit));
     const dim3 block(64 * kWaves);
-#define FEATHER_SMALLM_LAUNCH(BF, E4)                                                                       \
-    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, CT, LDSA, BF, E4>), grid, block, 0, stream, p.a, p.b, p.scale, \
-                       p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),     \
+#define FEATHER_SMALLM_LAUNCH(BF, E4, AB)                                                                          \
+    hipLaunchKernelGGL((scaled_mm_smallm_kernel<MT, CT, LDSA, BF, E4, AB>), grid, block, 0, stream, p.a, p.b,       \
+                       p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K),   \
                        p.has_scale, p.has_bias, nstrips, ksplit, partials, counters)
+    if (p.a_bf16) {
+        // bf16 activations: the LDS-activation variants, e5m2 weights
+        if constexpr (LDSA) {
+            if (p.b_e4m3) return false;
+            if (p.out_bf16) FEATHER_SMALLM_LAUNCH(true, false, true);
+            else FEATHER_SMALLM_LAUNCH(false, false, true);
+            return true;
+        }
+        return false;
+    }
     if (p.out_bf16) {
-        if (p.b_e4m3) FEATHER_SMALLM_LAUNCH(true, true);
-        else FEATHER_SMALLM_LAUNCH(true, false);
+        if (p.b_e4m3) FEATHER_SMALLM_LAUNCH(true, true, false);
+        else FEATHER_SMALLM_LAUNCH(true, false, false);
     } else {
-        if (p.b_e4m3) FEATHER_SMALLM_LAUNCH(false, true);
-        else FEATHER_SMALLM_LAUNCH(false, false);
+        if (p.b_e4m3) FEATHER_SMALLM_LAUNCH(false, true, false);
+        else FEATHER_SMALLM_LAUNCH(false, false, false);
     }
 #undef FEATHER_SMALLM_LAUNCH
+    return true;
 }
 
 int mt_of(int64_t M) { return static_cast<int>((M + 15) / 16); }
@@ -311,13 +322,11 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
         const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
         switch (mt) {
             case 3:
-                if (lds_a) launch_mt<3, ct_split(3), true>(p, ks, partials, counters, stream);
-                else launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream);
-                return true;
+                return lds_a ? launch_mt<3, ct_split(3), true>(p, ks, partials, counters, stream)
+                             : launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream);
             case 4:
-                if (lds_a) launch_mt<4, ct_split(4), true>(p, ks, partials, counters, stream);
-                else launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream);
-                return true;
+                return lds_a ? launch_mt<4, ct_split(4), true>(p, ks, partials, counters, stream)
+                             : launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream);
             default: return false;
         }
     }
@@ -326,16 +335,15 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
     const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
     switch (mt) {
         case 1:
-            if (lds_a) wide ? launch_mt<1, 4, true>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1, true>(p, 1, nullptr, nullptr, stream);
-            else wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream);
-            return true;
+            if (lds_a) return wide ? launch_mt<1, 4, true>(p, 1, nullptr, nullptr, stream)
+                                   : launch_mt<1, 1, true>(p, 1, nullptr, nullptr, stream);
+            return wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream);
         case 2:  // (the 2 x 4 tile keeps direct A loads: its LDS variant runs out of VGPRs)
-            if (wide) launch_mt<2, 4>(p, 1, nullptr, nullptr, stream);
-            else if (lds_a) launch_mt<2, 1, true>(p, 1, nullptr, nullptr, stream);
-            else launch_mt<2, 1>(p, 1, nullptr, nullptr, stream);
-            return true;
-        case 3: launch_mt<3, 1>(p, 1, nullptr, nullptr, stream); return true;
-        case 4: launch_mt<4, 1>(p, 1, nullptr, nullptr, stream); return true;
+            if (wide) return launch_mt<2, 4>(p, 1, nullptr, nullptr, stream);
+            return lds_a ? launch_mt<2, 1, true>(p, 1, nullptr, nullptr, stream)
+                         : launch_mt<2, 1>(p, 1, nullptr, nullptr, stream);
+        case 3: return launch_mt<3, 1>(p, 1, nullptr, nullptr, stream);
+        case 4: return launch_mt<4, 1>(p, 1, nullptr, nullptr, stream);
         default: return false;
     }
 }

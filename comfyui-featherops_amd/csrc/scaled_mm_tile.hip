@@ -237,6 +237,7 @@ void launch_tile(const MmArgs& p, hipStream_t stream) {
 }  // namespace
 
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
+    if (p.a_bf16) return false;  // fp16 activations only (bf16 is converted by the caller)
     switch (kernel_id) {
         case kTile256x256: launch_tile<256, 256, 2, 4>(p, stream); return true;
         case kTile256x128: launch_tile<256, 128, 4, 2>(p, stream); return true;

@@ -32,19 +32,23 @@ def _check(cond: bool, msg: str) -> None:
 
 
 def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
-                       b_dtype, require_cuda: bool = True, block_divisible: bool = True) -> None:
+                       b_dtype, require_cuda: bool = True, block_divisible: bool = True,
+                       allow_bf16_a: bool = False) -> None:
     """Raise RuntimeError with the reference's message for any argument the
     kernel cannot take. `require_cuda=False` skips the device checks;
     `block_divisible=False` replaces the BlockM/BlockN/ChunkK divisibility
     rules by what the gfx950 kernels need (N % 16 == 0; K % 16 is always
-    required) -- the any-M entry."""
+    required) and `allow_bf16_a` accepts bf16 activations -- the any-M entry."""
     if require_cuda:
         _check(a.is_cuda, "a must be a CUDA tensor")
         _check(b_prepacked.is_cuda, "b_prepacked must be a CUDA tensor")
         _check(c.is_cuda, "c must be a CUDA tensor")
         _check(b_prepacked.device == a.device, "b_prepacked must be on the same device as a")
         _check(c.device == a.device, "c must be on the same device as a")
-    _check(a.dtype == torch.float16, "a must be float16")
+    if allow_bf16_a:
+        _check(a.dtype in (torch.float16, torch.bfloat16), "a must be float16 or bfloat16")
+    else:
+        _check(a.dtype == torch.float16, "a must be float16")
     _check(c.dtype in (torch.float16, torch.bfloat16), "c must be float16 or bfloat16")
     _check(b_dtype in (0, 1), "b_dtype must be 0 (fp8e4m3) or 1 (fp8e5m2)")
     if b_dtype == 0:
@@ -290,20 +294,31 @@ def _any_m_op(
     if M == 0:
         return out
     cfg = any_m_config(M)
-    validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, 0 if b_prepacked.dtype == torch.float8_e4m3fn else 1,
-                       block_divisible=False)
+    b_dtype = 0 if b_prepacked.dtype == torch.float8_e4m3fn else 1
+    validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, b_dtype, block_divisible=False, allow_bf16_a=True)
     L = _lib.lib()
     dev = a.device
     with torch.cuda.device(dev):
         stream = _lib.stream_ptr(dev)
         ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
         ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
-        launched = L.feather_launch_scaled_mm_ws(
-            a.data_ptr(), b_prepacked.data_ptr(), scale.data_ptr() if scale is not None else None,
-            bias.data_ptr() if bias is not None else None, out.data_ptr(), M, N, K,
-            1 if scale is not None else 0, 1 if bias is not None else 0, *cfg,
-            0 if b_prepacked.dtype == torch.float8_e4m3fn else 1, 0 if out_dtype == torch.float16 else 1,
-            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
+
+        def launch(x, a_code):
+            return L.feather_launch_scaled_mm_ex(
+                x.data_ptr(), a_code, b_prepacked.data_ptr(), scale.data_ptr() if scale is not None else None,
+                bias.data_ptr() if bias is not None else None, out.data_ptr(), M, N, K,
+                1 if scale is not None else 0, 1 if bias is not None else 0, *cfg, b_dtype,
+                0 if out_dtype == torch.float16 else 1,
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
+
+        if a.dtype == torch.bfloat16:
+            # bf16 activations are rounded to fp16 inside the kernel where it has
+            # that variant; otherwise converted here first (ops.py:88's x.to(fp16))
+            launched = launch(a, _lib.DTYPE_CODES[torch.bfloat16])
+            if not launched:
+                launched = launch(a.to(torch.float16), _lib.DTYPE_CODES[torch.float16])
+        else:
+            launched = launch(a, _lib.DTYPE_CODES[torch.float16])
     _check(bool(launched), "Unsupported config")
     return out
 
@@ -316,7 +331,9 @@ def _(a, b_prepacked, scale, bias, out_dtype):
 def scaled_mm_hip_any_m(a, b_prepacked, scale, bias, out_dtype) -> torch.Tensor:
     """scaled_mm for any row count M, without padding A or slicing C (the
     kernels mask rows past M). Rows are independent, so the result equals
-    padding M to a block multiple, calling scaled_mm_hip and slicing."""
+    padding M to a block multiple, calling scaled_mm_hip and slicing. `a` may
+    also be bf16: it is then rounded to fp16 (round to nearest even) inside the
+    GEMM, the same values as calling it with a.to(torch.float16)."""
     return _any_m_op(a, b_prepacked, scale, bias, out_dtype)
 
 

@@ -61,10 +61,11 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
                       hipStream_t stream);
 
 /*
- * launch_scaled_mm with a caller workspace. For small M (M <= 64) the kernel
- * then also splits K across workgroups, which the weight-streaming regime
- * needs to keep every CU loading (the reference ABI has no workspace, so
- * launch_scaled_mm splits K inside each workgroup only). workspace_bytes must
+ * launch_scaled_mm with a caller workspace. For shapes too small to fill the
+ * GPU with output tiles (M <= 64, or fewer than 256 tiles of 128 x 128) the
+ * kernels then also split K across workgroups, which keeps every CU loading
+ * (the reference ABI has no workspace, so launch_scaled_mm runs those shapes
+ * without the cross-workgroup split). workspace_bytes must
  * be at least feather_scaled_mm_workspace_size(...) (0 means none needed; a
  * smaller workspace falls back to the unsplit kernel). The workspace must be
  * zero-filled before its first use and is left zero-filled by every call;
@@ -77,7 +78,28 @@ bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, cons
                                  int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
-/* Workspace bytes feather_launch_scaled_mm_ws can use for this call (0 = none). */
+/*
+ * feather_launch_scaled_mm_ws with the activation dtype as an argument:
+ * a_dtype FEATHER_DTYPE_F16 (same as feather_launch_scaled_mm_ws) or
+ * FEATHER_DTYPE_BF16 -- bf16 activations are rounded to fp16 inside the
+ * kernel with round-to-nearest-even, the values of the x.to(float16) that
+ * comfy_feather/ops.py:88 runs before the GEMM, so the separate cast pass
+ * over A disappears. bf16 activations are served for e5m2 weights by the
+ * split-K LDS-DMA tiles (K % 64 == 0) and the small-M kernel; any other
+ * combination returns false and launches nothing (the caller converts A and
+ * calls again). In practice the bf16 variants are the ones for small shapes
+ * (the small-M kernel and the split-K tiles), where the separate cast is a
+ * launch of its own; for large tiles converting every A-fragment read costs
+ * more than one cast pass. Same workspace contract. No counterpart in the
+ * reference.
+ */
+bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_prepacked, const float* scale,
+                                 const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale,
+                                 int has_bias, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m,
+                                 int repeat_n, int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
+/* Workspace bytes feather_launch_scaled_mm_ws / _ex can use for this call (0 = none). */
 size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
                                         int unroll_k, int repeat_m, int repeat_n);
 

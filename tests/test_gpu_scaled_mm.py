@@ -214,3 +214,29 @@ def test_small_m_split_k_workspace(cuda, M, N, K):
         # (small-M kernel); the first (N + 63) // 64 are counters either way
         tiles = (N + 63) // 64
         assert (ws[: tiles * 4] == 0).all(), "arrival counters must be left at zero"
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (16, 12288, 512), (48, 1024, 2048), (64, 1024, 1024),
+                                   (256, 768, 512), (1024, 4096, 1024), (100, 512, 1040)])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_bf16_activations(cuda, hk, M, N, K, out_dtype):
+    """bf16 A through the any-M entry: rounded to fp16 inside the kernel (or cast
+    first where the kernel has no bf16 variant) -- bit-identical to passing
+    a.to(float16), and within the gate of the oracle on the fp16-rounded A.
+    Includes values that overflow fp16 (1e6 -> inf), fp16 subnormals and zeros."""
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    a[0, :4] = torch.tensor([3.0e-6, -5.0e-8, 1.0e-9, 0.0]).bfloat16()
+    a[M - 1, 3] = 1.0e6 if M > 1 else a[M - 1, 3]
+    packed, s = weight_like(N, K, g)
+    bias, bias_np = _bias_for(out_dtype, N, g)
+    ad = a.to(cuda)
+    bd = to_dev_codes(packed, cuda).view(torch.float8_e5m2)
+    sd = torch.tensor(s, device=cuda)
+    y = hk.scaled_mm_hip_any_m(ad, bd, sd, bias.to(cuda), out_dtype)
+    y16 = hk.scaled_mm_hip_any_m(ad.to(torch.float16), bd, sd, bias.to(cuda), out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y16.view(torch.int16)), "bf16 A must equal the fp16 cast of A"
+    od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+    ref = O.scaled_mm_ref(a.to(torch.float16).numpy(), packed, s, bias_np, od)
+    assert_gemm_close(y, ref, out_dtype, f"bf16 A {M}x{N}x{K}")
