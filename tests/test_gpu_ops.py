@@ -113,22 +113,29 @@ def test_torch_compile_configured_and_autotuned(cuda, hk):
 
 
 def test_graph_capture_replays_match_eager(cuda, hk, quant):
-    """scaled_mm (small-M and tile kernels) and quantize captured in a HIP graph:
-    every replay, with eager work in between, equals the eager result."""
+    """scaled_mm (small-M kernel with and without its K split, split-K tiles,
+    bf16 activations) and quantize captured in a HIP graph: every replay, with
+    eager work in between, equals the eager result (the split paths' arrival
+    counters must come back to zero on every replay)."""
     g = torch.Generator(device=cuda).manual_seed(3)
     w = (torch.randn(512, 1024, generator=g, device=cuda) * 0.02).half()
     qt = quant.make_feather_quantized_weight(w, None, torch.float16)
     bp, scale = quant.get_feather_plain_tensors(qt)
     bias = (torch.randn(512, generator=g, device=cuda) * 0.01).half()
-    for m, cfg in ((16, (1, 1, 2, 1, 2)), (512, (2, 4, 4, 8, 4))):
+    for m, cfg in ((16, (1, 1, 2, 1, 2)), (48, (1, 1, 2, 1, 2)), (512, (2, 4, 4, 8, 4)), (40, None)):
         a = torch.randn(m, 1024, generator=g, device=cuda).half()
-        eager = hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg)
+        if cfg is None:  # any-M entry with bf16 activations (small-M kernel, K split across workgroups)
+            a = a.bfloat16()
+            fn = lambda: hk.scaled_mm_hip_any_m(a, bp, scale, bias, torch.float16)  # noqa: E731
+        else:
+            fn = lambda: hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg)  # noqa: E731
+        eager = fn()
         out = torch.empty_like(eager)
-        hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg)  # warm the op before capture
+        fn()  # warm the op before capture
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            out.copy_(hk.scaled_mm_hip_configured(a, bp, scale, bias, torch.float16, *cfg))
+            out.copy_(fn())
         for rep in range(4):
             out.zero_()
             graph.replay()
