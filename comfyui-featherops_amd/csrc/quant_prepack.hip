@@ -211,8 +211,12 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
     // scale_in: caller-supplied scale (quant.py:59-62), no recalculation and no clamp
     const float s = scale_in ? scale_in[0] : scale_from_amax<DT>(amax_bits[0], native != 0);
     if (scale_out && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) scale_out[0] = s;
-    const int n = blockIdx.y * 64 + (threadIdx.x & 63);
-    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // thread t takes row n0 + t / 4 and K group i0 + t % 4: a wave's loads
+    // cover 16 whole 128-byte row segments (16 cache lines per instruction
+    // instead of 64 with one row per lane), and its stores 4 runs of 16
+    // consecutive 16-byte chunks
+    const int n = blockIdx.y * 64 + (threadIdx.x >> 2);
+    const int i = blockIdx.x * 4 + (threadIdx.x & 3);
     if (n >= N || i >= (K >> 4)) return;
 
     float v[16];
