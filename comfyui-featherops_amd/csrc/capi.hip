@@ -17,7 +17,7 @@ struct Cfg {
 };
 
 // Reference configurations (kernel/hip/hip_kernel.py:60-89, hip_kernel.cu:603-630)
-// followed by three gfx950 tiles the reference has no tuple for.
+// followed by four gfx950 tiles the reference has no tuple for.
 constexpr Cfg kConfigs[] = {
     {1, 1, 2, 1, 2}, {1, 1, 4, 1, 2}, {1, 2, 2, 1, 2}, {1, 2, 4, 1, 2}, {1, 4, 2, 1, 2}, {1, 4, 4, 1, 2},
     {1, 8, 2, 1, 2}, {1, 8, 4, 1, 2}, {1, 1, 2, 2, 2}, {1, 1, 4, 2, 2}, {1, 1, 2, 4, 4}, {1, 1, 4, 4, 4},

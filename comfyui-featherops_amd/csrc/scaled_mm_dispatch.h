@@ -32,7 +32,7 @@ enum KernelId : int {
     kTile128x128 = 4,
     kTile64x128 = 5,
     kTile64x64 = 6,
-    kSmallM = 10,  // M <= 64: split-K inside the workgroup, one 16-column strip per workgroup
+    kSmallM = 10,  // M <= 64: K split inside the workgroup (and across workgroups with a workspace), 16- or 64-column strips
     // LDS-DMA pipelined tiles (K % 64 == 0)
     kLds256x256w2x4 = 20,
     kLds256x256w4x2 = 21,
@@ -46,8 +46,8 @@ enum KernelId : int {
 };
 
 // Every launcher returns false, and launches nothing, for a variant it does not
-// have (bf16 activations are served by the LDS-DMA and small-M kernels with
-// e5m2 weights only).
+// have (bf16 activations are served by the split-K LDS tiles and the small-M
+// kernel with e5m2 weights only).
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
 // Small-M kernel. With a workspace of at least smallm_workspace_bytes() it
 // also splits K across workgroups; without one it splits K inside each
