@@ -263,7 +263,15 @@ int feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream
     if (n < 0 || (n > 0 && (!in || !out))) return FEATHER_ERR_INVALID;
     if ((reinterpret_cast<uintptr_t>(in) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
     if (n == 0) return FEATHER_OK;
-    feather::launch_bf16_to_fp16(in, out, n, stream);
+    feather::launch_bf16_to_fp16(in, out, n, false, stream);
+    return launch_status();
+}
+
+int feather_bf16_to_fp16_rne(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream) {
+    if (n < 0 || (n > 0 && (!in || !out))) return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(in) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
+    if (n == 0) return FEATHER_OK;
+    feather::launch_bf16_to_fp16(in, out, n, true, stream);
     return launch_status();
 }
 

@@ -24,7 +24,8 @@ struct QuantArgs {
 void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream);
 void launch_chunk_transpose(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int dir, hipStream_t stream);
 void launch_prepack_kn(const uint8_t* src, uint8_t* dst, int64_t K, int64_t N, hipStream_t stream);
-void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+// rne = false: round toward zero (kernel/convert.py); true: round to nearest even (torch's .to(float16))
+void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, bool rne, hipStream_t stream);
 void launch_dequant(const uint8_t* src, const float* scale, void* dst, int64_t N, int64_t K, int dtype,
                     hipStream_t stream);
 

@@ -293,28 +293,46 @@ __global__ __launch_bounds__(256) void prepack_kn_bytes_kernel(const uint8_t* __
     }
 }
 
-// bf16 -> fp16 with round-toward-zero (v_cvt_pkrtz_f16_f32): values beyond
-// the fp16 range saturate to +-65504, inf stays inf, NaN stays NaN.
+// bf16 -> fp16. kRne = false: round toward zero (v_cvt_pkrtz_f16_f32), values
+// beyond the fp16 range saturate to +-65504, inf stays inf, NaN stays NaN
+// (kernel/convert.py). kRne = true: round to nearest even with overflow to
+// +-inf (v_cvt_pk_f16_f32), torch's x.to(float16) (comfy_feather/ops.py:88).
+template <bool kRne>
+__device__ __forceinline__ uint32_t bf16x2_to_fp16x2(uint32_t w) {
+    const float lo = bits_f32(w << 16);
+    const float hi = bits_f32(w & 0xffff0000u);
+    if constexpr (kRne) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    }
+}
+
+template <bool kRne>
 __global__ __launch_bounds__(256) void bf16_to_fp16_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                                            int64_t n) {
     const int64_t nvec = n / 8;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < nvec; g += stride) {
-        const uint4 t = reinterpret_cast<const uint4*>(in)[g];
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float lo = bits_f32(w[h] << 16);
-            const float hi = bits_f32(w[h] & 0xffff0000u);
-            o[h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-        }
-        reinterpret_cast<uint4*>(out)[g] = make_uint4(o[0], o[1], o[2], o[3]);
+    const uint4* in4 = reinterpret_cast<const uint4*>(in);
+    uint4* out4 = reinterpret_cast<uint4*>(out);
+    auto cvt = [](uint4 t) {
+        return make_uint4(bf16x2_to_fp16x2<kRne>(t.x), bf16x2_to_fp16x2<kRne>(t.y), bf16x2_to_fp16x2<kRne>(t.z),
+                          bf16x2_to_fp16x2<kRne>(t.w));
+    };
+    int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    for (; g + 3 * stride < nvec; g += 4 * stride) {  // four 16-byte loads in flight
+        const uint4 t0 = in4[g], t1 = in4[g + stride], t2 = in4[g + 2 * stride], t3 = in4[g + 3 * stride];
+        out4[g] = cvt(t0);
+        out4[g + stride] = cvt(t1);
+        out4[g + 2 * stride] = cvt(t2);
+        out4[g + 3 * stride] = cvt(t3);
     }
+    for (; g < nvec; g += stride) out4[g] = cvt(in4[g]);
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t e = nvec * 8 + threadIdx.x;
-        const float f = bits_f32(static_cast<uint32_t>(in[e]) << 16);
-        out[e] = static_cast<uint16_t>(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f, 0.0f)) & 0xffffu);
+        out[e] = static_cast<uint16_t>(bf16x2_to_fp16x2<kRne>(in[e]) & 0xffffu);
     }
 }
 
@@ -404,8 +422,10 @@ void launch_prepack_kn(const uint8_t* src, uint8_t* dst, int64_t K, int64_t N, h
     }
 }
 
-void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream) {
-    hipLaunchKernelGGL(bf16_to_fp16_kernel, dim3(grid_for(n / 8, 256, 8192)), dim3(256), 0, stream, in, out, n);
+void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, bool rne, hipStream_t stream) {
+    const dim3 grid(grid_for(n / 32, 256, 4096));
+    if (rne) hipLaunchKernelGGL(bf16_to_fp16_kernel<true>, grid, dim3(256), 0, stream, in, out, n);
+    else hipLaunchKernelGGL(bf16_to_fp16_kernel<false>, grid, dim3(256), 0, stream, in, out, n);
 }
 
 void launch_dequant(const uint8_t* src, const float* scale, void* dst, int64_t N, int64_t K, int dtype,

@@ -38,6 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     "feather_unprepack_transpose": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "feather_prepack_b": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "feather_bf16_to_fp16": (_int, [_vp, _vp, _i64, _vp]),
+    "feather_bf16_to_fp16_rne": (_int, [_vp, _vp, _i64, _vp]),
     "feather_dequantize_e5m2": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp]),
     "feather_status_string": (ctypes.c_char_p, [_int]),
     "feather_abi_version": (_int, []),

@@ -313,10 +313,14 @@ def _any_m_op(
 
         if a.dtype == torch.bfloat16:
             # bf16 activations are rounded to fp16 inside the kernel where it has
-            # that variant; otherwise converted here first (ops.py:88's x.to(fp16))
+            # that variant; otherwise converted here first by the library's
+            # round-to-nearest cast (the values of ops.py:88's x.to(float16))
             launched = launch(a, _lib.DTYPE_CODES[torch.bfloat16])
             if not launched:
-                launched = launch(a.to(torch.float16), _lib.DTYPE_CODES[torch.float16])
+                a16 = torch.empty(a.shape, dtype=torch.float16, device=dev)
+                _lib.check(L.feather_bf16_to_fp16_rne(a.data_ptr(), a16.data_ptr(), a.numel(), stream),
+                           "feather_bf16_to_fp16_rne")
+                launched = launch(a16, _lib.DTYPE_CODES[torch.float16])
         else:
             launched = launch(a, _lib.DTYPE_CODES[torch.float16])
     _check(bool(launched), "Unsupported config")

@@ -150,6 +150,13 @@ int feather_prepack_b(const uint8_t* b_kn, uint8_t* out, int64_t K, int64_t N, h
  * (bf16_to_fp16); n may be any count, buffers 16-byte aligned. */
 int feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
 
+/* bf16 -> fp16, round to nearest even, overflow to +-inf: the values of
+ * torch's x.to(float16), which comfy_feather/ops.py:88 applies to bf16
+ * activations before the GEMM. The any-M Python entry uses it where the GEMM
+ * kernel has no bf16-activation variant. n any count, buffers 16-byte aligned.
+ * No counterpart in the reference (it uses the torch cast). */
+int feather_bf16_to_fp16_rne(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+
 /* (K/16, N, 16) e5m2 -> (N, K) of out_dtype as out_dtype(float32(q) * scale).
  * Replaces quant.py:99-102 (FeatherFP8E5M2PackedLayout.dequantize). */
 int feather_dequantize_e5m2(const uint8_t* packed, const float* scale, void* out, int out_dtype, int64_t N, int64_t K,

@@ -9,6 +9,9 @@ from oracle import feather_oracle as O
 
 
 def lib():
+    import __graft_entry__
+
+    __graft_entry__.load_package()  # the plugin directory as `featherops_amd`
     from featherops_amd.kernel.hip import _lib
 
     return _lib.lib()

@@ -190,6 +190,27 @@ def test_bf16_to_fp16_exhaustive(cuda, pkg):
         assert np.array_equal(o[~nan[:n]], z[:n][~nan[:n]])
 
 
+def test_bf16_to_fp16_rne_exhaustive(cuda, pkg):
+    """Round-to-nearest cast (the any-M entry's stand-in for ops.py:88's
+    x.to(float16)): all 65,536 bf16 patterns equal torch's CPU cast (NaN -> NaN),
+    plus a large array (4 loads in flight per thread) and odd tails."""
+    x_cpu = torch.from_numpy(ALL16.view(np.int16).copy()).view(torch.bfloat16)
+    want = x_cpu.to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(want.view(np.float16))
+    for n in (65536, 1, 7, 9, 1023):
+        xs = x_cpu[:n].to(cuda)
+        out = torch.empty(n, dtype=torch.float16, device=cuda)
+        assert lib().feather_bf16_to_fp16_rne(xs.data_ptr(), out.data_ptr(), n, stream(cuda)) == 0
+        torch.cuda.synchronize()
+        o = out.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(o[~nan[:n]], want[:n][~nan[:n]]), n
+        assert np.isnan(o[nan[:n]].view(np.float16)).all()
+    xr = torch.randn(3, 1 << 20, dtype=torch.bfloat16, device=cuda) * 3000
+    out = torch.empty(xr.shape, dtype=torch.float16, device=cuda)
+    assert lib().feather_bf16_to_fp16_rne(xr.data_ptr(), out.data_ptr(), xr.numel(), stream(cuda)) == 0
+    assert torch.equal(out, xr.to(torch.float16))
+
+
 def test_config5_weight_on_device(cuda, quant):
     """Config 5 quantizes 5120x13824 weights on the device: sampled rows vs the oracle."""
     gd = torch.Generator(device=cuda).manual_seed(5)
