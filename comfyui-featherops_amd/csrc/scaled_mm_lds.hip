@@ -184,7 +184,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         for (int rm = 0; rm < RM; ++rm) dst[rm] = *reinterpret_cast<const uint4*>(sa + a_lds(rm, kh));
     };
     // MFMAs of one K half: widen this half of the B operands, then run every
-    // M repeat; `hook(rm)` runs before the MFMAs of repeat rm.
+    // M repeat; `hook(rm)` runs before the MFMAs of repeat rm. The widened
+    // weights are the MFMA's first operand and the activations its second, so
+    // each 16x16 result is C^T: lane (lr, lg) element i is C[row lr][col
+    // 4*lg + i] of the tile. Measured 1.8% faster than the other operand order
+    // on M=32768 N=13824 K=5120 (the kernel is power-bound with random data).
     auto mm_half = [&](int kh, const uint4 (&araw)[RM], const uint4 (&braw)[RN], auto hook) {
         half8_t bq[RN];
 #pragma unroll
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             hook(rm);
             const half8_t a = a_frag<kABf16>(araw[rm]);
 #pragma unroll
-            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(a, bq[rn], acc[rm][rn]);
+            for (int rn = 0; rn < RN; ++rn) acc[rm][rn] = mfma16x16x32(bq[rn], a, acc[rm][rn]);
         }
     };
 
@@ -351,12 +355,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     for (int rm = 0; rm < RM; ++rm) {
 #pragma unroll
         for (int rn = 0; rn < RN; ++rn) {
+            uint32_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float v = kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s;
-                *reinterpret_cast<uint16_t*>(sc + (4 * lg + i) * kCRowBytes + (rn * 16 + lr) * 2) =
-                    f32_to_out_bits<kBf16>(v);
+                o[i] = f32_to_out_bits<kBf16>(v);
             }
+            // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
+            *reinterpret_cast<uint2*>(sc + lr * kCRowBytes + (rn * 16 + 4 * lg) * 2) =
+                make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
         }
         __syncthreads();
         const int out_row0 = m0 + wave_m * WTM + rm * 16;

@@ -168,8 +168,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
                     const half8_t b1 = widen_fp8x8<kE4m3>(braw[u][ct].z, braw[u][ct].w);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
-                        acc[mt][ct] = mfma16x16x32(a_frag<kABf16>(araw[u][mt][0]), b0, acc[mt][ct]);
-                        acc[mt][ct] = mfma16x16x32(a_frag<kABf16>(araw[u][mt][1]), b1, acc[mt][ct]);
+                        acc[mt][ct] = mfma16x16x32(b0, a_frag<kABf16>(araw[u][mt][0]), acc[mt][ct]);
+                        acc[mt][ct] = mfma16x16x32(b1, a_frag<kABf16>(araw[u][mt][1]), acc[mt][ct]);
                     }
                 }
             }
@@ -177,13 +177,15 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
     }
 
     if constexpr (kLdsA) __syncthreads();  // the reduction buffer overlays other waves' slabs
-    // accumulator element i of lane (lr, lg) is (row 4*lg + i, col lr) of its 16x16 tile
+    // weights are the MFMA's first operand, activations its second (as in the
+    // large-tile kernel), so accumulator element i of lane (lr, lg) is
+    // (row lr, col 4*lg + i) of its 16x16 tile
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][mt * 16 + 4 * lg + i][ct * 16 + lr] = acc[mt][ct][i];
+            for (int i = 0; i < 4; ++i) red[wave][mt * 16 + lr][ct * 16 + 4 * lg + i] = acc[mt][ct][i];
     __syncthreads();
 
     const int tile_elems = M * kCols;
