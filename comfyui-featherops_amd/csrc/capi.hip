@@ -111,6 +111,19 @@ int kernel_for(int64_t M, int64_t N, int64_t K, int wm, int wn, int rm, int rn) 
 
 bool is_splitk(int kid) { return kid == feather::kLdsSk64x64 || kid == feather::kLdsSk32x128; }
 
+// Compute units of the current device (256 on an MI355X), read once per device.
+int device_cus() {
+    constexpr int kMaxDevices = 64;
+    static int cus[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
 }  // namespace
@@ -296,6 +309,45 @@ const char* feather_status_string(int status) {
         case FEATHER_ERR_LAUNCH: return "kernel launch failed";
         default: return "unknown status";
     }
+}
+
+int feather_scaled_mm_pick_config(int64_t M, int64_t N, int64_t K, int* cfg) {
+    if (!cfg || M < 0 || !sizes_ok(M, N, K)) return FEATHER_ERR_INVALID;
+    // Output tiles, their measured throughput per CU relative to 256 x 256
+    // (M=32768, N=13824, K=5120 and M=4096, N=3072, K=3072 on MI355X), and the
+    // tuple that selects them. Cost of a tile = waves of workgroups x tile
+    // area / relative throughput; shapes too small for any of them are routed
+    // to the split-K tiles by the dispatcher whatever the tuple.
+    struct Cand {
+        Cfg c;
+        int bm, bn;
+        double eff;
+    };
+    static const Cand cands[] = {
+        {{2, 4, 4, 8, 4}, 256, 256, 1.00}, {{2, 4, 4, 8, 3}, 256, 192, 0.85}, {{2, 4, 4, 4, 4}, 128, 256, 0.90},
+        {{4, 2, 4, 4, 4}, 256, 128, 0.84}, {{2, 2, 4, 4, 4}, 128, 128, 0.80},
+    };
+    Cfg best = {1, 1, 2, 1, 2};  // M <= 64: the small-M kernel
+    if (M > 64) {
+        const int cus = device_cus();
+        double best_cost = 0.0;
+        bool have = false;
+        for (const Cand& c : cands) {
+            const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+            const double cost = static_cast<double>((tiles + cus - 1) / cus) * c.bm * c.bn / c.eff;
+            if (!have || cost < best_cost) {
+                best = c.c;
+                best_cost = cost;
+                have = true;
+            }
+        }
+    }
+    cfg[0] = best.wm;
+    cfg[1] = best.wn;
+    cfg[2] = best.u;
+    cfg[3] = best.rm;
+    cfg[4] = best.rn;
+    return FEATHER_OK;
 }
 
 int feather_abi_version(void) { return 1; }

@@ -16,6 +16,8 @@ ctypes on torch's current stream; there is no other compute path.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -271,13 +273,28 @@ def scaled_mm_hip(
 # any-M entry (no M padding): the gfx950 kernels mask rows past M
 # ---------------------------------------------------------------------------
 
-# (small-M kernel, 256x256 tile) picked by M; their tuples are in _CONFIGS
-_ANY_M_SMALL = (1, 1, 2, 1, 2)
-_ANY_M_LARGE = (2, 4, 4, 8, 4)
+# The any-M entry's configuration: the library's shape-based pick
+# (feather_scaled_mm_pick_config: the output tile whose waves x tile cost is
+# smallest on this device), cached per shape and device.
+_PICKED: dict = {}
 
 
-def any_m_config(M: int) -> tuple:
-    return _ANY_M_SMALL if M <= 64 else _ANY_M_LARGE
+def any_m_config(M: int, N: int, K: int, device: torch.device | None = None) -> tuple:
+    dev = device.index if device is not None and device.index is not None else (
+        torch.cuda.current_device() if torch.cuda.is_available() else -1)
+    key = (dev, M, N, K)
+    cfg = _PICKED.get(key)
+    if cfg is None:
+        out = (ctypes.c_int * 5)()
+        if dev >= 0:
+            with torch.cuda.device(dev):
+                status = _lib.lib().feather_scaled_mm_pick_config(M, N, K, out)
+        else:
+            status = _lib.lib().feather_scaled_mm_pick_config(M, N, K, out)
+        _lib.check(status, "feather_scaled_mm_pick_config")
+        cfg = tuple(out)
+        _PICKED[key] = cfg
+    return cfg
 
 
 @torch.library.custom_op("feather_ops_internal::scaled_mm_any_m", mutates_args=())
@@ -293,7 +310,7 @@ def _any_m_op(
     out = torch.empty((M, N), device=a.device, dtype=out_dtype)
     if M == 0:
         return out
-    cfg = any_m_config(M)
+    cfg = any_m_config(M, N, K, a.device)
     b_dtype = 0 if b_prepacked.dtype == torch.float8_e4m3fn else 1
     validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, b_dtype, block_divisible=False, allow_bf16_a=True)
     L = _lib.lib()

@@ -99,6 +99,17 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
                                  int repeat_n, int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/*
+ * A configuration tuple for this shape on the current device, without timing
+ * anything: the output tile whose waves of workgroups times tile cost is
+ * smallest (256x256, 256x192, 128x256, 256x128 or 128x128; the small-M
+ * kernel's tuple for M <= 64). Writes 5 ints (block_warps_m, block_warps_n,
+ * unroll_k, repeat_m, repeat_n) to cfg. The tuple ignores the reference's
+ * block-divisibility rule (for the any-M entry). No counterpart in the
+ * reference; the autotuner (kernel/hip/utils.py:192-223) times configs instead.
+ */
+int feather_scaled_mm_pick_config(int64_t M, int64_t N, int64_t K, int* cfg);
+
 /* Workspace bytes feather_launch_scaled_mm_ws / _ex can use for this call (0 = none). */
 size_t feather_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
                                         int unroll_k, int repeat_m, int repeat_n);

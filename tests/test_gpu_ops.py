@@ -159,7 +159,7 @@ def test_any_m_equals_padded(cuda, hk, M):
     s = torch.tensor(0.5, device=cuda)
     bias = torch.randn(N, generator=g, device=cuda).half()
     y = hk.scaled_mm_hip_any_m(a, bp, s, bias, torch.float16)
-    cfg = hk.any_m_config(M)
+    cfg = hk.any_m_config(M, N, K)
     bm = 16 * cfg[0] * cfg[3]
     mp = (M + bm - 1) // bm * bm
     ap = torch.nn.functional.pad(a, (0, 0, 0, mp - M))

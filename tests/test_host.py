@@ -69,6 +69,16 @@ def test_kernel_id_mapping(hk):
         assert hk.kernel_id(1024, 1024, 1024, cfg) == 30
 
 
+def test_pick_config(hk):
+    """The any-M entry's shape-based tile pick (256 CUs assumed without a GPU)."""
+    assert hk.any_m_config(32768, 13824, 5120) == (2, 4, 4, 8, 4)  # 256x256, 27 full waves
+    assert hk.any_m_config(4096, 3072, 3072) == (2, 4, 4, 8, 3)  # 256x192: 256 tiles, one per CU
+    assert hk.any_m_config(512, 9216, 3072) == (2, 4, 4, 4, 4)  # 128x256: 144 tiles in one wave
+    assert hk.any_m_config(16, 4096, 4096) == (1, 1, 2, 1, 2)  # small-M kernel
+    for shape in [(100, 3072, 3072), (1000, 5120, 13824), (65, 768, 512)]:
+        assert tuple(hk.any_m_config(*shape)) in set(hk._CONFIGS)
+
+
 def test_configs_keep_reference_entries(hk):
     ref = {(1, 1, 2, 1, 2), (1, 1, 4, 1, 2), (1, 2, 2, 1, 2), (1, 2, 4, 1, 2), (1, 4, 2, 1, 2), (1, 4, 4, 1, 2),
            (1, 8, 2, 1, 2), (1, 8, 4, 1, 2), (1, 1, 2, 2, 2), (1, 1, 4, 2, 2), (1, 1, 2, 4, 4), (1, 1, 4, 4, 4),
