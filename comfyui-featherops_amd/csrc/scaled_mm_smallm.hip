@@ -21,6 +21,8 @@
 //     counter for the next call. Partials and counters use device-coherent
 //     (agent-scope) loads, stores and atomics; the splits of a strip are also
 //     placed on one XCD (workgroup p runs on XCD p % 8).
+#include <cstdlib>
+
 #include "feather_common.h"
 #include "lds_dma.h"
 #include "scaled_mm_dispatch.h"
@@ -235,21 +237,11 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
         __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Shape policy (measured on MI355X, M=16..64, weights rotated past the MALL):
-//   * K is split across workgroups only for M > 32, where the activation
-//     re-reads dominate; for M <= 32 the arrival/reduction round trip costs
-//     more than it saves;
-//   * without a workgroup K split, strips are widened to 64 columns only when
-//     that still leaves >= 192 workgroups (N >= 12288), otherwise every CU is
-//     needed and strips stay 16 columns wide.
+// Shape policy for M > 32 (measured on MI355X, weights rotated past the
+// MALL): strips of 32 columns, K split across workgroups up to the workgroup
+// target. For M <= 32 see smallm_plan's cost model.
 constexpr int kSplitMinMt = 3;
-constexpr int kWideStripMinGroups = 192;
 constexpr int ct_split(int mt) { return mt <= 2 ? 4 : 2; }
-
-int ct_unsplit(int mt, int64_t N) {
-    if (mt <= 2 && (N + 63) / 64 >= kWideStripMinGroups) return 4;
-    return 1;
-}
 
 template <int MT, int CT, bool LDSA = false>
 bool launch_mt(const MmArgs& p, int ksplit, float* partials, uint32_t* counters, hipStream_t stream) {
@@ -285,67 +277,120 @@ int mt_of(int64_t M) { return static_cast<int>((M + 15) / 16); }
 
 }  // namespace
 
-int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups) {
-    if (M <= 0 || M > 64 || mt_of(M) < kSplitMinMt) return 1;
-    const int ct = ct_split(mt_of(M));
+struct SmallmPlan {
+    int ct;  // column tiles per strip (strip = 16 * ct columns)
+    int ks;  // workgroups per strip (K split)
+};
+
+// Cost model for M <= 32, in microseconds, fitted to MI355X runs over
+// M = 1..32, N = 3072..13824, K = 3072..13824 with rotated weights. A
+// workgroup holds 128 KB of LDS, so one runs per CU and a grid larger than
+// the CU count runs in rounds. Each wave keeps a fixed number of 16-byte
+// weight loads in flight, so a workgroup's rate is bounded by its bytes in
+// flight over the loaded HBM latency: a 16-column strip (one load per stage
+// per wave) streams 1 KB of weight per ~0.052 us, a 64-column strip (twice
+// the loads in flight) per ~0.027 us. On top of that: ~3.1 us per round
+// (launch, first-load latency, reduction and epilogue), a whole-chip ceiling
+// of ~7 TB/s, and ~2.6 us for a K split across workgroups (partials out,
+// arrival counter, last-arriver sum).
+double smallm_cost_us(int64_t N, int64_t nst, int ct, int ks, int cus) {
     const int64_t nstrips = (N + 16 * ct - 1) / (16 * ct);
+    const int64_t groups = nstrips * ks;
+    const int64_t rounds = (groups + cus - 1) / cus;
+    const double kb_per_group = static_cast<double>(ct) * static_cast<double>((nst + ks - 1) / ks);
+    const double per_kb = ct >= 4 ? 0.027 : 0.052;
+    const double t_rounds = static_cast<double>(rounds) * (3.1 + kb_per_group * per_kb);
+    const double t_chip = 3.1 + static_cast<double>(nst) * static_cast<double>(N) * 1024.0 / 16.0 / 7.0e6;
+    return (t_rounds > t_chip ? t_rounds : t_chip) + (ks > 1 ? 2.6 : 0.0);
+}
+
+SmallmPlan smallm_plan(int64_t M, int64_t N, int64_t K, int target_groups, bool allow_split = true) {
+    const int mt = mt_of(M);
     const int64_t nst = (K + 63) / 64;
-    int64_t ks = (target_groups + nstrips - 1) / nstrips;
     // each split keeps at least one 64-K stage per wave
-    const int64_t max_ks = nst / kWaves > 0 ? nst / kWaves : 1;
-    if (ks > max_ks) ks = max_ks;
-    if (ks > 8) ks = 8;
-    return ks < 1 ? 1 : static_cast<int>(ks);
+    int64_t max_ks = nst / kWaves > 0 ? nst / kWaves : 1;
+    if (max_ks > 8) max_ks = 8;
+    if (!allow_split) max_ks = 1;
+    SmallmPlan pl{1, 1};
+    if (M <= 0 || M > 64) return pl;
+    const int cus = target_groups > 0 ? target_groups : 256;
+    if (mt >= kSplitMinMt) {
+        pl.ct = ct_split(mt);
+        const int64_t nstrips = (N + 16 * pl.ct - 1) / (16 * pl.ct);
+        int64_t ks = (cus + nstrips - 1) / nstrips;
+        if (ks > max_ks) ks = max_ks;
+        pl.ks = ks < 1 ? 1 : static_cast<int>(ks);
+    } else {
+        double best = smallm_cost_us(N, nst, 1, 1, cus);
+        for (int ct : {1, 4})
+            for (int ks = 1; ks <= max_ks; ++ks) {
+                const double c = smallm_cost_us(N, nst, ct, ks, cus);
+                if (c < best) {
+                    best = c;
+                    pl = SmallmPlan{ct, ks};
+                }
+            }
+    }
+#ifdef FEATHER_SMALLM_PROBE
+    if (const char* e = std::getenv("FEATHEROPS_SMALLM_CT")) pl.ct = std::atoi(e);
+    if (const char* e = std::getenv("FEATHEROPS_SMALLM_KS")) pl.ks = std::atoi(e);
+#endif
+    return pl;
+}
+
+int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups) {
+    return smallm_plan(M, N, K, target_groups).ks;
 }
 
 size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups) {
-    const int ks = smallm_ksplit(M, N, K, target_groups);
-    if (ks <= 1) return 0;
-    const int ct = ct_split(mt_of(M));
-    const int64_t nstrips = (N + 16 * ct - 1) / (16 * ct);
+    const SmallmPlan pl = smallm_plan(M, N, K, target_groups);
+    if (pl.ks <= 1) return 0;
+    const int64_t nstrips = (N + 16 * pl.ct - 1) / (16 * pl.ct);
     // counters first (256-byte aligned), then ksplit partial tiles per strip
     const size_t counter_bytes = (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256;
-    return counter_bytes + static_cast<size_t>(nstrips) * ks * M * 16 * ct * 4;
+    return counter_bytes + static_cast<size_t>(nstrips) * pl.ks * M * 16 * pl.ct * 4;
 }
 
 bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (p.M <= 0 || p.M > 64) return false;
     const int mt = mt_of(p.M);
     const int target = p.smallm_min_groups > 0 ? p.smallm_min_groups : 256;
-    int ks = smallm_ksplit(p.M, p.N, p.K, target);
-    if (ks > 1 && (workspace == nullptr || workspace_bytes < smallm_workspace_bytes(p.M, p.N, p.K, target)))
-        ks = 1;  // no (or too small a) workspace: split K inside each workgroup only
-    if (ks > 1) {
-        const int ct = ct_split(mt);
-        const int64_t nstrips = (p.N + 16 * ct - 1) / (16 * ct);
-        uint32_t* counters = static_cast<uint32_t*>(workspace);
-        float* partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                                   (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256);
-        const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
-        switch (mt) {
-            case 3:
-                return lds_a ? launch_mt<3, ct_split(3), true>(p, ks, partials, counters, stream)
-                             : launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream);
-            case 4:
-                return lds_a ? launch_mt<4, ct_split(4), true>(p, ks, partials, counters, stream)
-                             : launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream);
-            default: return false;
-        }
+    SmallmPlan pl = smallm_plan(p.M, p.N, p.K, target);
+    float* partials = nullptr;
+    uint32_t* counters = nullptr;
+    if (pl.ks > 1 && (workspace == nullptr || workspace_bytes < smallm_workspace_bytes(p.M, p.N, p.K, target))) {
+        // no (or too small a) workspace: split K inside each workgroup only
+        pl = smallm_plan(p.M, p.N, p.K, target, false);
+        if (mt >= kSplitMinMt) pl = SmallmPlan{1, 1};
     }
-    const bool wide = ct_unsplit(mt, p.N) == 4;
+    if (pl.ks > 1) {
+        const int64_t nstrips = (p.N + 16 * pl.ct - 1) / (16 * pl.ct);
+        counters = static_cast<uint32_t*>(workspace);
+        partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                            (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256);
+    }
+    const int ks = pl.ks;
+    const bool wide = pl.ct >= 2;
     // A through LDS needs every byte offset into A to fit the copy's 32-bit lane offset
     const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
     switch (mt) {
         case 1:
-            if (lds_a) return wide ? launch_mt<1, 4, true>(p, 1, nullptr, nullptr, stream)
-                                   : launch_mt<1, 1, true>(p, 1, nullptr, nullptr, stream);
-            return wide ? launch_mt<1, 4>(p, 1, nullptr, nullptr, stream) : launch_mt<1, 1>(p, 1, nullptr, nullptr, stream);
+            if (lds_a) return wide ? launch_mt<1, 4, true>(p, ks, partials, counters, stream)
+                                   : launch_mt<1, 1, true>(p, ks, partials, counters, stream);
+            return wide ? launch_mt<1, 4>(p, ks, partials, counters, stream)
+                        : launch_mt<1, 1>(p, ks, partials, counters, stream);
         case 2:  // (the 2 x 4 tile keeps direct A loads: its LDS variant runs out of VGPRs)
-            if (wide) return launch_mt<2, 4>(p, 1, nullptr, nullptr, stream);
-            return lds_a ? launch_mt<2, 1, true>(p, 1, nullptr, nullptr, stream)
-                         : launch_mt<2, 1>(p, 1, nullptr, nullptr, stream);
-        case 3: return launch_mt<3, 1>(p, 1, nullptr, nullptr, stream);
-        case 4: return launch_mt<4, 1>(p, 1, nullptr, nullptr, stream);
+            if (wide) return launch_mt<2, 4>(p, ks, partials, counters, stream);
+            return lds_a ? launch_mt<2, 1, true>(p, ks, partials, counters, stream)
+                         : launch_mt<2, 1>(p, ks, partials, counters, stream);
+        case 3:
+            if (wide) return lds_a ? launch_mt<3, ct_split(3), true>(p, ks, partials, counters, stream)
+                                   : launch_mt<3, ct_split(3)>(p, ks, partials, counters, stream);
+            return launch_mt<3, 1>(p, ks, partials, counters, stream);
+        case 4:
+            if (wide) return lds_a ? launch_mt<4, ct_split(4), true>(p, ks, partials, counters, stream)
+                                   : launch_mt<4, ct_split(4)>(p, ks, partials, counters, stream);
+            return launch_mt<4, 1>(p, ks, partials, counters, stream);
         default: return false;
     }
 }

@@ -182,7 +182,8 @@ def test_baseline_config4_video_dit(cuda, K, N):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (16, 3072, 3072), (1, 1040, 2048), (33, 2000, 4096),
-                                   (64, 4096, 4096), (48, 12288, 2048), (16, 128, 128)])
+                                   (64, 4096, 4096), (48, 12288, 2048), (16, 128, 128), (16, 5120, 13824),
+                                   (1, 3072, 12288), (32, 5120, 13824), (7, 2000, 8192)])
 def test_small_m_split_k_workspace(cuda, M, N, K):
     """feather_launch_scaled_mm_ws: K split across workgroups through the
     workspace; twice in a row (the arrival counters must come back to zero)."""
@@ -209,8 +210,8 @@ def test_small_m_split_k_workspace(cuda, M, N, K):
         outs.append(c)
     assert torch.equal(outs[0], outs[1]), "split-K reduction must be deterministic"
     if nbytes:
-        # split across workgroups (M > 32): the workspace starts with one arrival
-        # counter per 64-column tile (LDS split-K path) or per 32-column strip
+        # split across workgroups: the workspace starts with one arrival counter
+        # per 64-column tile (LDS split-K path) or per 32- or 64-column strip
         # (small-M kernel); the first (N + 63) // 64 are counters either way
         tiles = (N + 63) // 64
         assert (ws[: tiles * 4] == 0).all(), "arrival counters must be left at zero"

@@ -162,3 +162,17 @@ def test_ops_m_padding_rule(pkg):
     from featherops_amd.comfy_feather import ops
 
     assert [ops._m_block(m) for m in (1, 64, 65, 128, 129, 256, 257)] == [16, 16, 32, 32, 64, 64, 128]
+
+
+def test_small_m_plan_workspace(pkg):
+    """Small-M plan (256-CU target without a GPU): a K split across
+    workgroups, which needs a workspace, only where it balances the grid."""
+    from featherops_amd.kernel.hip import _lib
+
+    lib = _lib.lib()
+    cfg = (1, 1, 2, 1, 2)
+    assert lib.feather_scaled_mm_workspace_size(16, 4096, 4096, *cfg) == 0  # 256 strips: one per CU
+    assert lib.feather_scaled_mm_workspace_size(16, 13824, 5120, *cfg) == 0  # 216 strips of 64 columns
+    # 80 strips of 64 columns x 3 K ranges: counters (256-aligned) + 3 fp32 partial tiles per strip
+    assert lib.feather_scaled_mm_workspace_size(16, 5120, 13824, *cfg) == 512 + 80 * 3 * 16 * 64 * 4
+    assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 256 + 48 * 4 * 1 * 64 * 4
