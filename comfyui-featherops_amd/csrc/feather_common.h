@@ -87,15 +87,27 @@ __device__ __forceinline__ half8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
 // output type: both operands to fp32 (exact), add, one rounding to the output
 // type. For fp16 this equals a native fp16 add (24 >= 2*11+2 bits).
 template <bool kBf16>
-__device__ __forceinline__ void add_bias8(uint4& v, const uint16_t* bias) {
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+__device__ __forceinline__ void add_bias8(uint4& v, uint4 b) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+    uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float lo = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] & 0xffffu)) + out_bits_to_f32<kBf16>(bias[2 * i]);
-        const float hi = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] >> 16)) + out_bits_to_f32<kBf16>(bias[2 * i + 1]);
-        w[i] = static_cast<uint32_t>(f32_to_out_bits<kBf16>(lo)) | (static_cast<uint32_t>(f32_to_out_bits<kBf16>(hi)) << 16);
+        const float lo = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] & 0xffffu)) +
+                         out_bits_to_f32<kBf16>(static_cast<uint16_t>(bw[i] & 0xffffu));
+        const float hi = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] >> 16)) +
+                         out_bits_to_f32<kBf16>(static_cast<uint16_t>(bw[i] >> 16));
+        o[i] = static_cast<uint32_t>(f32_to_out_bits<kBf16>(lo)) | (static_cast<uint32_t>(f32_to_out_bits<kBf16>(hi)) << 16);
     }
-    v = make_uint4(w[0], w[1], w[2], w[3]);
+    v = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// bias[0..7] packed two per word (bias needs only 2-byte alignment)
+__device__ __forceinline__ uint4 load_bias8(const uint16_t* bias) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = static_cast<uint32_t>(bias[2 * i]) | (static_cast<uint32_t>(bias[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 __device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }

@@ -24,6 +24,17 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // memory accesses across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Orders a wave's LDS writes before its own later LDS reads of them (by any
+// lane of the same wave): the writes are waited for (lgkmcnt(0)) and the
+// compiler may not move LDS accesses across. Enough when each wave stages
+// through its own LDS region; no workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // A rows are 128 bytes (8 chunks of 16 B); chunk c of row r sits at c ^ swz(r).

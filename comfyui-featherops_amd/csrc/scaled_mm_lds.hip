@@ -64,9 +64,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     constexpr int kBPerWave = (kBInst + kWaves - 1) / kWaves;
     constexpr int kLoadsPerStage = kAPerWave + kBPerWave;
     static_assert(BN % 64 == 0, "a B copy must stay inside one K group");
-    constexpr int kCRowBytes = WTN * 2 + 16;
-    constexpr int kCWaveBytes = 16 * kCRowBytes;
-    static_assert(kWaves * kCWaveBytes <= kStage, "epilogue staging reuses stage buffer 0");
     // One LDS object per stage buffer (the main loop is unrolled by three).
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf1[kStage];
@@ -354,14 +351,32 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             __hip_atomic_store(&counters[lin], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // ---- epilogue (LDS reused after every wave is past its last stage) ----
-    stage_barrier();
-    uint8_t* sc = sbuf0 + wave * kCWaveBytes;
+    // ---- epilogue: each wave stages its whole WTM x WTN output tile in LDS
+    // (the stage buffers, free once every wave is past its last stage) with
+    // one wait, then stores rows of WTN * 2 contiguous bytes ----
     const int out_col0 = n0 + wave_n * WTN;
-    constexpr int kChunksPerRow = WTN / 8;
-    constexpr int kChunks = 16 * kChunksPerRow;
+    constexpr int kCPR = WTN / 8;                // 16-byte chunks per staged row
+    constexpr int kRowBytes = WTN * 2;
+    constexpr int kRowsPerStore = 64 / kCPR;     // rows one store instruction covers
+    constexpr int kLanesUsed = kRowsPerStore * kCPR;
+    constexpr int kWaveBytes = WTM * kRowBytes;
+    constexpr int kWavesPerBuf = kStage / kWaveBytes;
+    static_assert(3 * kWavesPerBuf >= kWaves, "epilogue staging must fit the stage buffers");
+    const int cc = lane % kCPR;  // this lane's chunk of every row it stores
+    const int rsub = lane / kCPR;
+    const int gcol = out_col0 + cc * 8;
+    // the bias chunk is issued before the barrier and waited for after the
+    // staging writes, so its latency overlaps them
+    const uint4 b8 = has_bias && lane < kLanesUsed && gcol < N ? load_bias8(bias + gcol) : make_uint4(0u, 0u, 0u, 0u);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's last operand reads are done
+    stage_barrier();
+    uint8_t* sc = (wave / kWavesPerBuf == 0 ? sbuf0 : wave / kWavesPerBuf == 1 ? sbuf1 : sbuf2) +
+                  (wave % kWavesPerBuf) * kWaveBytes;
+    // chunk c of staged row r sits at (c + r) % kCPR (spreads the rows of one
+    // write over the LDS banks)
 #pragma unroll
     for (int rm = 0; rm < RM; ++rm) {
+        const int row = rm * 16 + lr;
 #pragma unroll
         for (int rn = 0; rn < RN; ++rn) {
             uint32_t o[4];
@@ -371,24 +386,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
                 o[i] = f32_to_out_bits<kBf16>(v);
             }
             // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
-            *reinterpret_cast<uint2*>(sc + lr * kCRowBytes + (rn * 16 + 4 * lg) * 2) =
+            const int chunk = (2 * rn + (lg >> 1) + row) % kCPR;
+            *reinterpret_cast<uint2*>(sc + row * kRowBytes + chunk * 16 + (lg & 1) * 8) =
                 make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
         }
-        __syncthreads();
-        const int out_row0 = m0 + wave_m * WTM + rm * 16;
+    }
+    // staging writes and the bias load complete: one wait, then no vmcnt wait
+    // between the stores (vmcnt counts stores too)
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    wave_lds_sync();                     // each wave reads only its own region
+    const int out_row0 = m0 + wave_m * WTM;
 #pragma unroll
-        for (int c = lane; c < kChunks; c += 64) {
-            const int r = c / kChunksPerRow;
-            const int cc = c % kChunksPerRow;
-            uint4 v = *reinterpret_cast<const uint4*>(sc + r * kCRowBytes + cc * 16);
-            const int grow = out_row0 + r;
-            const int gcol = out_col0 + cc * 8;
-            if (grow < M && gcol < N) {
-                if (has_bias) add_bias8<kBf16>(v, bias + gcol);
-                *reinterpret_cast<uint4*>(C + static_cast<int64_t>(grow) * N + gcol) = v;
-            }
+    for (int p = 0; p < (WTM + kRowsPerStore - 1) / kRowsPerStore; ++p) {
+        const int r = p * kRowsPerStore + rsub;
+        const int grow = out_row0 + r;
+        if (lane < kLanesUsed && r < WTM && grow < M && gcol < N) {
+            uint4 v = *reinterpret_cast<const uint4*>(sc + r * kRowBytes + ((cc + r) % kCPR) * 16);
+            if (has_bias) add_bias8<kBf16>(v, b8);
+            *reinterpret_cast<uint4*>(C + static_cast<int64_t>(grow) * N + gcol) = v;
         }
-        __syncthreads();
     }
 }
 

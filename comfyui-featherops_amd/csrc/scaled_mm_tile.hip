@@ -24,6 +24,7 @@
 //   * epilogue goes through LDS so every lane writes 16 contiguous bytes.
 // Any M (rows past M are masked), N % 16 == 0 and K % 16 == 0 are accepted.
 #include "feather_common.h"
+#include "lds_dma.h"
 #include "scaled_mm_dispatch.h"
 
 namespace feather {
@@ -182,6 +183,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_tile_kernel(
     const int out_col0 = n0 + wave_n * WTN;
     constexpr int kChunksPerRow = WTN / 8;          // 16-byte chunks per staged row
     constexpr int kChunks = 16 * kChunksPerRow;     // per M repeat
+    // this lane's bias chunks, loaded once (the same columns for every M repeat)
+    constexpr int kLaneChunks = (kChunks + 63) / 64;
+    uint4 bias8[kLaneChunks];
+#pragma unroll
+    for (int j = 0; j < kLaneChunks; ++j) {
+        const int c = lane + 64 * j;
+        const int gcol = out_col0 + (c % kChunksPerRow) * 8;
+        bias8[j] = has_bias && c < kChunks && gcol < N ? load_bias8(bias + gcol) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // Wait for the bias here, once: a wait inside the store loop would also
+    // wait for every C store issued before it (vmcnt counts stores too) and
+    // serialise the stores.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 #pragma unroll
     for (int rm = 0; rm < RM; ++rm) {
         // accumulator (row 4*lg+i, col lr) of each 16x16 tile -> rounded output bits in LDS
@@ -195,21 +209,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_tile_kernel(
                     f32_to_out_bits<kBf16>(v);
             }
         }
-        __syncthreads();
+        wave_lds_sync();  // each wave stages through its own LDS region
         const int out_row0 = m0 + wave_m * WTM + rm * 16;
 #pragma unroll
-        for (int c = lane; c < kChunks; c += 64) {
+        for (int j = 0; j < kLaneChunks; ++j) {
+            const int c = lane + 64 * j;
             const int r = c / kChunksPerRow;
             const int cc = c % kChunksPerRow;
-            uint4 v = *reinterpret_cast<const uint4*>(sc + r * kCRowBytes + cc * 16);
             const int grow = out_row0 + r;
             const int gcol = out_col0 + cc * 8;
-            if (grow < M && gcol < N) {
-                if (has_bias) add_bias8<kBf16>(v, bias + gcol);
+            if (c < kChunks && grow < M && gcol < N) {
+                uint4 v = *reinterpret_cast<const uint4*>(sc + r * kCRowBytes + cc * 16);
+                if (has_bias) add_bias8<kBf16>(v, bias8[j]);
                 *reinterpret_cast<uint4*>(C + static_cast<int64_t>(grow) * N + gcol) = v;
             }
         }
-        __syncthreads();
+        wave_lds_sync();  // each wave stages through its own LDS region
     }
 }
 
