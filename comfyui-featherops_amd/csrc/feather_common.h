@@ -43,10 +43,30 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> bf16 bits packed (a in the low half), the same values as
+// f32_to_bf16_bits: round to nearest even by one v_cvt_pk_bf16_f32, then NaN
+// replaced by the canonical 0x7fc0.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    if (a != a) r = (r & 0xffff0000u) | 0x7fc0u;
+    if (b != b) r = (r & 0x0000ffffu) | 0x7fc00000u;
+    return r;
+}
+
 template <bool kBf16>
 __device__ __forceinline__ uint16_t f32_to_out_bits(float f) {
     if constexpr (kBf16) return f32_to_bf16_bits(f);
     else return f32_to_half_bits(f);
+}
+// Two fp32 -> output bits packed (a in the low half), rounded to nearest even.
+template <bool kBf16>
+__device__ __forceinline__ uint32_t f32x2_to_out_bits(float a, float b) {
+    if constexpr (kBf16) return f32x2_to_bf16x2_bits(a, b);
+    else return static_cast<uint32_t>(f32_to_half_bits(a)) | (static_cast<uint32_t>(f32_to_half_bits(b)) << 16);
 }
 template <bool kBf16>
 __device__ __forceinline__ float out_bits_to_f32(uint16_t b) {
@@ -97,7 +117,7 @@ __device__ __forceinline__ void add_bias8(uint4& v, uint4 b) {
                          out_bits_to_f32<kBf16>(static_cast<uint16_t>(bw[i] & 0xffffu));
         const float hi = out_bits_to_f32<kBf16>(static_cast<uint16_t>(w[i] >> 16)) +
                          out_bits_to_f32<kBf16>(static_cast<uint16_t>(bw[i] >> 16));
-        o[i] = static_cast<uint32_t>(f32_to_out_bits<kBf16>(lo)) | (static_cast<uint32_t>(f32_to_out_bits<kBf16>(hi)) << 16);
+        o[i] = f32x2_to_out_bits<kBf16>(lo, hi);
     }
     v = make_uint4(o[0], o[1], o[2], o[3]);
 }

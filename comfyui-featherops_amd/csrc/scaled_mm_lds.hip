@@ -379,16 +379,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         const int row = rm * 16 + lr;
 #pragma unroll
         for (int rn = 0; rn < RN; ++rn) {
-            uint32_t o[4];
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s;
-                o[i] = f32_to_out_bits<kBf16>(v);
-            }
+            for (int i = 0; i < 4; ++i) v[i] = kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s;
             // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
             const int chunk = (2 * rn + (lg >> 1) + row) % kCPR;
             *reinterpret_cast<uint2*>(sc + row * kRowBytes + chunk * 16 + (lg & 1) * 8) =
-                make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                make_uint2(f32x2_to_out_bits<kBf16>(v[0], v[1]), f32x2_to_out_bits<kBf16>(v[2], v[3]));
         }
     }
     // staging writes and the bias load complete: one wait, then no vmcnt wait
