@@ -176,7 +176,7 @@ def _quantize_2d(w2d: torch.Tensor, native: bool, ckpt_scale: torch.Tensor | Non
                                                               out.data_ptr(), stream), "quantize_prepack")
             return out, given_scale
         scale_out = torch.empty((), dtype=torch.float32, device=dev)
-        workspace = torch.empty(1, dtype=torch.int32, device=dev)
+        workspace = torch.empty(256, dtype=torch.int32, device=dev)  # partial maxima (1 KB)
         cs = None
         if ckpt_scale is not None:
             cs = ckpt_scale.reshape(1).to(device=dev, dtype=torch.float32).contiguous()

@@ -24,6 +24,15 @@ constexpr int kNumXcd = 8;
 __device__ __forceinline__ uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 
+// Returns x as computed, in an fp32 register. Placed between a multiply and a
+// narrowing conversion it stops the compiler from fusing the two into one
+// mixed-precision FMA: that FMA adds +0, which turns an exact -0 product
+// into +0.
+__device__ __forceinline__ float opaque_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 __device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

@@ -17,7 +17,7 @@ struct QuantArgs {
     bool native;              // false: load path (fp32), true: patch path (weight dtype)
     uint8_t* out;             // (K/16, N, 16) e5m2 bytes
     float* scale_out;         // device scalar
-    uint32_t* workspace;      // >= 4 bytes of device memory (unused when scale_in is set)
+    uint32_t* workspace;      // >= 1024 bytes of device memory: partial maxima (unused when scale_in is set)
     const float* scale_in;    // device scalar: use this scale instead of recalculating (native only)
 };
 

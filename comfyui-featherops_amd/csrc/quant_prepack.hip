@@ -95,7 +95,12 @@ __device__ __forceinline__ void load16(const void* p, int64_t i, float (&v)[16])
     }
 }
 
-__global__ void zero_word_kernel(uint32_t* w) { w[0] = 0u; }
+// The amax pass writes one partial maximum per workgroup (plain stores: no
+// atomics on one address, which serialise in L2, and nothing to clear first);
+// a one-workgroup kernel reduces them into word 0, which every quantize
+// workgroup reads.
+constexpr int kAmaxParts = 256;
+constexpr int kAmaxThreads = 1024;
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
@@ -140,10 +145,10 @@ __device__ __forceinline__ float abs_bits_to_f32(uint32_t m) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ w, int64_t n,
+__global__ __launch_bounds__(kAmaxThreads) void amax_kernel(const void* __restrict__ w, int64_t n,
                                                    const float* __restrict__ ckpt_scale, int premul,
-                                                   uint32_t* __restrict__ amax_bits) {
-    __shared__ uint32_t part[4];
+                                                   uint32_t* __restrict__ amax_parts) {
+    __shared__ uint32_t part[kAmaxThreads / 64];
     const float cs = (premul && ckpt_scale) ? ckpt_scale[0] : 1.0f;
     const bool per_element = premul && !(__builtin_fabsf(cs) <= 3.402823466e38f);  // inf or NaN scale
     uint32_t m = 0u;
@@ -152,16 +157,15 @@ __global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ w, i
     const uint4* v16 = static_cast<const uint4*>(w);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     if (!per_element) {
-        // native-bit maximum, four 16-byte loads in flight per thread
-        int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-        for (; i + 3 * stride < nvec; i += 4 * stride) {
-            const uint4 t0 = v16[i], t1 = v16[i + stride], t2 = v16[i + 2 * stride], t3 = v16[i + 3 * stride];
-            m = abs_max_words<DT>(t0, m);
-            m = abs_max_words<DT>(t1, m);
-            m = abs_max_words<DT>(t2, m);
-            m = abs_max_words<DT>(t3, m);
+        // native-bit maximum, four 16-byte loads in flight per thread (also in
+        // the last, partial round: a zero word leaves the maximum unchanged)
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += 4 * stride) {
+            uint4 t[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) t[u] = i + u * stride < nvec ? v16[i + u * stride] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m = abs_max_words<DT>(t[u], m);
         }
-        for (; i < nvec; i += stride) m = abs_max_words<DT>(v16[i], m);
         if (blockIdx.x == 0 && threadIdx.x < n - nvec * kPerVec) {
             const int64_t t = nvec * kPerVec + threadIdx.x;
             const uint32_t b = DT == kDtypeF32 ? (static_cast<const uint32_t*>(w)[t] & 0x7fffffffu)
@@ -183,8 +187,8 @@ __global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ w, i
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t r = part[0];
-        for (int i = 1; i < 4; ++i) r = part[i] > r ? part[i] : r;
-        atomicMax(amax_bits, r);
+        for (int i = 1; i < kAmaxThreads / 64; ++i) r = part[i] > r ? part[i] : r;
+        amax_parts[blockIdx.x] = r;
     }
 }
 
@@ -199,6 +203,19 @@ __device__ __forceinline__ float scale_from_amax(uint32_t amax_bits, bool native
         s = 1.0f / r;
     }
     return s;
+}
+
+// Reduces the amax pass's partial maxima into word 0 (one workgroup).
+__global__ __launch_bounds__(kAmaxParts) void amax_finalize_kernel(uint32_t* __restrict__ parts, int nparts) {
+    __shared__ uint32_t red[kAmaxParts / 64];
+    uint32_t m = static_cast<int>(threadIdx.x) < nparts ? parts[threadIdx.x] : 0u;
+    m = wave_max_u32(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kAmaxParts / 64; ++k) m = red[k] > m ? red[k] : m;
+        parts[0] = m;
+    }
 }
 
 // grid: (ceil(K/16 / 4), ceil(N / 64)); block 256 = 64 rows (n) x 4 K-groups.
@@ -225,7 +242,7 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
     if (native) {
         const float inv = WeightType<DT>::round(1.0f / s);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2(WeightType<DT>::round(v[j] * inv));
+        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2(WeightType<DT>::round(opaque_f32(v[j] * inv)));
     } else {
         const float cs = ckpt_scale ? ckpt_scale[0] : 1.0f;
         const float inv = 1.0f / s;
@@ -351,7 +368,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const uint16_t h = static_cast<uint16_t>(((w[j >> 2] >> (8 * (j & 3))) & 0xffu) << 8);
-        v[j] = half_bits_to_f32(h) * s;
+        v[j] = opaque_f32(half_bits_to_f32(h) * s);  // a -0 code stays -0
     }
     const int64_t base = static_cast<int64_t>(n) * K + i * 16;
     if constexpr (DT == kDtypeF32) {
@@ -384,10 +401,14 @@ template <int DT>
 void launch_quant(const QuantArgs& q, hipStream_t stream) {
     const int64_t n = q.N * q.K;
     const bool premul = !q.native;
+    // amax workgroups: one round of four 16-byte loads per thread covers
+    // 1024 * 4 * 16 bytes; at most kAmaxParts workgroups, looping over the rest
+    const int64_t round_elems = static_cast<int64_t>(kAmaxThreads) * 4 * (DT == kDtypeF32 ? 4 : 8);
+    const int nparts = q.scale_in ? 0 : grid_for(n, static_cast<int>(round_elems), kAmaxParts);
     if (!q.scale_in) {
-        hipLaunchKernelGGL(zero_word_kernel, dim3(1), dim3(1), 0, stream, q.workspace);
-        hipLaunchKernelGGL((amax_kernel<DT>), dim3(grid_for(n / 32, 256, 2048)), dim3(256), 0, stream, q.w, n,
-                           q.ckpt_scale, premul ? 1 : 0, q.workspace);
+        hipLaunchKernelGGL((amax_kernel<DT>), dim3(nparts), dim3(kAmaxThreads), 0, stream, q.w, n, q.ckpt_scale,
+                           premul ? 1 : 0, q.workspace);
+        hipLaunchKernelGGL(amax_finalize_kernel, dim3(1), dim3(kAmaxParts), 0, stream, q.workspace, nparts);
     }
     const dim3 grid(static_cast<uint32_t>((q.K / 16 + 3) / 4), static_cast<uint32_t>((q.N + 63) / 64));
     hipLaunchKernelGGL((quant_prepack_kernel<DT>), grid, dim3(256), 0, stream, q.w, static_cast<int>(q.N),

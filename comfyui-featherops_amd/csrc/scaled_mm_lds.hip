@@ -381,7 +381,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         for (int rn = 0; rn < RN; ++rn) {
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s;
+            for (int i = 0; i < 4; ++i) v[i] = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
             // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
             const int chunk = (2 * rn + (lg >> 1) + row) % kCPR;
             *reinterpret_cast<uint2*>(sc + row * kRowBytes + chunk * 16 + (lg & 1) * 8) =

@@ -133,8 +133,9 @@ int feather_scaled_mm_kernel_id(int64_t M, int64_t N, int64_t K, int block_warps
  *   native = 1: patch path, quantize_feather_weight (quant.py:139-146):
  *               arithmetic in w's dtype, fp16 reciprocal clamp (quant.py:56-58)
  * w_dtype: FEATHER_DTYPE_F16 / _BF16 / _F32. K % 16 == 0, w 16-byte aligned.
- * scale_out receives the fp32 scale. workspace: >= 4 bytes of device memory,
- * overwritten (cleared by a kernel, no hipMemset). Returns a status code.
+ * scale_out receives the fp32 scale. workspace: >= 1024 bytes of device
+ * memory, overwritten (per-workgroup partial maxima of |w|; no clearing
+ * needed). Returns a status code.
  */
 int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,
                                   int native, uint8_t* out, float* scale_out, uint32_t* workspace, hipStream_t stream);

@@ -164,6 +164,9 @@ def test_dequantize(cuda, quant, dtype, code):
         g = got.numpy()
         assert np.array_equal(np.isnan(g), np.isnan(ref))
         assert np.array_equal(g[~np.isnan(g)], ref[~np.isnan(ref)])
+        # signed zeros too: code 0x80 is -0 and must dequantize to -0
+        assert np.array_equal(np.signbit(g[~np.isnan(g)]), np.signbit(ref[~np.isnan(ref)]))
+        assert np.signbit(g[codes == 0x80]).all() and (codes == 0x80).any()
     sd = quant.FeatherFP8E5M2PackedLayout.state_dict_tensors(packed, params)
     assert np.array_equal(_bytes(sd[""]), codes)
 

@@ -117,6 +117,28 @@ def test_special_weights(cuda):
     assert_gemm_close(capi_scaled_mm(ad, bd, None, bias.to(cuda), torch.float16), ref, torch.float16)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,cfg", [(256, 256, (2, 4, 4, 8, 4)), (16, 256, (1, 1, 2, 1, 2)),
+                                     (64, 256, (1, 8, 4, 8, 2)), (256, 272, (2, 4, 4, 8, 4))])
+def test_signed_zero_outputs(cuda, M, K, cfg, out_dtype):
+    """Zero rows of A under a negative scale: the oracle's fp32 product 0 * s
+    is -0, so every output of those rows is -0 (sign bit set) on every path:
+    LDS tiles, small-M kernel, split-K tiles, register-staged tile (K % 64)."""
+    g = torch.Generator().manual_seed(11)
+    N = 256
+    a = torch.randn(M, K, generator=g).half()
+    a[::3] = 0.0
+    packed, _ = weight_like(N, K, g)
+    s = -0.75
+    ref = O.scaled_mm_ref(a.numpy(), packed, np.float32(s), None, O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16)
+    y = capi_scaled_mm(a.to(cuda), to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), None, out_dtype, cfg)
+    bits = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref_bits = ref.view(np.uint16) if ref.dtype == np.float16 else ref
+    assert (ref_bits[::3] == 0x8000).all(), "oracle: 0 * negative scale is -0"
+    assert np.array_equal(bits[::3], ref_bits[::3]), f"signed zeros {M}x{K} {cfg}"
+    assert_gemm_close(y, ref, out_dtype, f"negative scale {M}x{K} {cfg}")
+
+
 def test_inf_nan_propagation(cuda):
     M, K, N = 64, 128, 64
     a = torch.ones(M, K, dtype=torch.float16)
