@@ -33,6 +33,35 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+_OUT_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _valid_fast(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
+                block_divisible, allow_bf16_a) -> bool:
+    """True when every check of validate_scaled_mm passes (device, dtypes,
+    shapes, strides, alignment, divisibility); one expression, no messages.
+    False sends the caller to the full checks, which name what failed."""
+    if a.dim() != 2 or b_prepacked.dim() != 3 or c.dim() != 2:
+        return False
+    M, K = a.shape
+    Kg, N, sixteen = b_prepacked.shape
+    dev = a.device
+    bm = 16 * block_warps_m * repeat_m
+    bn = 16 * block_warps_n * repeat_n
+    return (dev.type == "cuda" and b_prepacked.device == dev and c.device == dev
+            and (a.dtype == torch.float16 or (allow_bf16_a and a.dtype == torch.bfloat16))
+            and c.dtype in _OUT_DTYPES
+            and ((b_dtype == 1 and b_prepacked.dtype == torch.float8_e5m2)
+                 or (b_dtype == 0 and b_prepacked.dtype == torch.float8_e4m3fn))
+            and K % 16 == 0 and Kg == K // 16 and sixteen == 16 and tuple(c.shape) == (M, N)
+            and a.stride() == (K, 1) and b_prepacked.stride() == (N * 16, 16, 1) and c.stride() == (N, 1)
+            and (scale is None or (scale.device == dev and scale.dtype == torch.float32 and scale.numel() == 1))
+            and (bias is None or (bias.device == dev and bias.dtype == c.dtype and bias.numel() == N))
+            and a.data_ptr() % 16 == 0 and b_prepacked.data_ptr() % 16 == 0 and c.data_ptr() % 16 == 0
+            and ((M % bm == 0 and N % bn == 0 and K % (16 * unroll_k) == 0) if block_divisible else N % 16 == 0)
+            and 32 * block_warps_m * block_warps_n <= 1024)
+
+
 def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
                        b_dtype, require_cuda: bool = True, block_divisible: bool = True,
                        allow_bf16_a: bool = False) -> None:
@@ -41,6 +70,9 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     `block_divisible=False` replaces the BlockM/BlockN/ChunkK divisibility
     rules by what the gfx950 kernels need (N % 16 == 0; K % 16 is always
     required) and `allow_bf16_a` accepts bf16 activations -- the any-M entry."""
+    if require_cuda and _valid_fast(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m,
+                                    repeat_n, b_dtype, block_divisible, allow_bf16_a):
+        return
     if require_cuda:
         _check(a.is_cuda, "a must be a CUDA tensor")
         _check(b_prepacked.is_cuda, "b_prepacked must be a CUDA tensor")
@@ -116,6 +148,22 @@ def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     return ws
 
 
+class _NoSwitch:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_SWITCH = _NoSwitch()
+
+
+def _on_device(dev: torch.device):
+    """torch.cuda.device(dev) unless dev is already the current device."""
+    return _NO_SWITCH if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+
 def _scaled_mm_native(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
                       b_dtype) -> None:
     validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
@@ -124,7 +172,8 @@ def _scaled_mm_native(a, b_prepacked, scale, bias, c, block_warps_m, block_warps
     dev = a.device
     M, K = a.shape
     N = b_prepacked.shape[1]
-    with torch.cuda.device(dev):
+    # the launch goes to the current HIP device: switch only when a lives elsewhere
+    with _on_device(dev):
         stream = _lib.stream_ptr(dev)
         ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m,
                                                       repeat_n)
@@ -315,7 +364,7 @@ def _any_m_op(
     validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, b_dtype, block_divisible=False, allow_bf16_a=True)
     L = _lib.lib()
     dev = a.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         stream = _lib.stream_ptr(dev)
         ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
         ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
