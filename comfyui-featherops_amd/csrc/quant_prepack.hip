@@ -15,11 +15,11 @@
 // c10 conversion: round to nearest even, |x| >= 61440 -> +-inf, NaN -> 0x7f
 // with the sign bit kept.
 //
-// Two kernels: a grid-stride amax that folds per-workgroup maxima into one
-// 32-bit word with a vector atomicMax, then a streaming quantize that
-// recomputes the scale from that word in every thread and writes the
-// prepacked bytes directly (16 output bytes per thread, 1 KB contiguous per
-// wave).
+// Three kernels: a grid-stride amax that writes one partial maximum per
+// workgroup, a one-workgroup reduction of those partials into one 32-bit
+// word, then a streaming quantize that recomputes the scale from that word in
+// every thread and writes the prepacked bytes directly (16 output bytes per
+// thread, 1 KB contiguous per wave).
 #include "feather_common.h"
 #include "quant_prepack.h"
 
