@@ -338,15 +338,15 @@ __global__ __launch_bounds__(256) void bf16_to_fp16_kernel(const uint16_t* __res
         return make_uint4(bf16x2_to_fp16x2<kRne>(t.x), bf16x2_to_fp16x2<kRne>(t.y), bf16x2_to_fp16x2<kRne>(t.z),
                           bf16x2_to_fp16x2<kRne>(t.w));
     };
-    int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    for (; g + 3 * stride < nvec; g += 4 * stride) {  // four 16-byte loads in flight
-        const uint4 t0 = in4[g], t1 = in4[g + stride], t2 = in4[g + 2 * stride], t3 = in4[g + 3 * stride];
-        out4[g] = cvt(t0);
-        out4[g + stride] = cvt(t1);
-        out4[g + 2 * stride] = cvt(t2);
-        out4[g + 3 * stride] = cvt(t3);
+    // four 16-byte loads in flight per thread, also in the last, partial round
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < nvec; g += 4 * stride) {
+        uint4 t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = g + u * stride < nvec ? in4[g + u * stride] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (g + u * stride < nvec) out4[g + u * stride] = cvt(t[u]);
     }
-    for (; g < nvec; g += stride) out4[g] = cvt(in4[g]);
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t e = nvec * 8 + threadIdx.x;
         out[e] = static_cast<uint16_t>(bf16x2_to_fp16x2<kRne>(in[e]) & 0xffffu);
@@ -444,7 +444,7 @@ void launch_prepack_kn(const uint8_t* src, uint8_t* dst, int64_t K, int64_t N, h
 }
 
 void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, bool rne, hipStream_t stream) {
-    const dim3 grid(grid_for(n / 32, 256, 4096));
+    const dim3 grid(grid_for(n / 32, 256, 8192));
     if (rne) hipLaunchKernelGGL(bf16_to_fp16_kernel<true>, grid, dim3(256), 0, stream, in, out, n);
     else hipLaunchKernelGGL(bf16_to_fp16_kernel<false>, grid, dim3(256), 0, stream, in, out, n);
 }
