@@ -263,3 +263,56 @@ def test_bf16_activations(cuda, hk, M, N, K, out_dtype):
     od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
     ref = O.scaled_mm_ref(a.to(torch.float16).numpy(), packed, s, bias_np, od)
     assert_gemm_close(y, ref, out_dtype, f"bf16 A {M}x{N}x{K}")
+
+
+def test_validation_fast_path_matches_full(cuda, hk):
+    """The one-expression fast path of validate_scaled_mm accepts valid CUDA
+    arguments and rejects every argument the full checks reject (which then
+    raise the reference's message)."""
+    M, N, K = 64, 128, 256
+
+    def good():
+        return dict(a=torch.empty(M, K, dtype=torch.float16, device=cuda),
+                    b=torch.empty(K // 16, N, 16, dtype=torch.float8_e5m2, device=cuda),
+                    scale=torch.ones((), dtype=torch.float32, device=cuda),
+                    bias=torch.zeros(N, dtype=torch.float16, device=cuda),
+                    c=torch.empty(M, N, dtype=torch.float16, device=cuda), cfg=(1, 1, 2, 1, 2), b_dtype=1)
+
+    def fast(x, **kw):
+        return hk._valid_fast(x["a"], x["b"], x["scale"], x["bias"], x["c"], *x["cfg"], x["b_dtype"],
+                              kw.get("block_divisible", True), kw.get("allow_bf16_a", False))
+
+    x = good()
+    assert fast(x)
+    misaligned = torch.empty(M * K + 1, dtype=torch.float16, device=cuda)[1:].view(M, K)
+    mutations = [
+        (dict(a=x["a"].float()), "a must be float16"),
+        (dict(a=x["a"].bfloat16()), "a must be float16"),
+        (dict(c=x["c"].float()), "c must be float16 or bfloat16"),
+        (dict(b=x["b"].view(torch.uint8)), "b_prepacked must be float8_e5m2"),
+        (dict(b_dtype=0), "b_prepacked must be float8_e4m3fn"),
+        (dict(a=x["a"][:, :128]), r"b_prepacked.shape\[0\] must equal K/16"),
+        (dict(c=torch.empty(32, N, dtype=torch.float16, device=cuda)), r"c.shape\[0\] must equal M"),
+        (dict(a=torch.empty(K, M, dtype=torch.float16, device=cuda).t()), r"a.stride\(0\) must equal K"),
+        (dict(c=torch.empty(N, M, dtype=torch.float16, device=cuda).t()), r"c.stride\(0\) must equal N"),
+        (dict(scale=torch.ones(2, device=cuda)), "scale must have one element"),
+        (dict(scale=torch.ones((), dtype=torch.float16, device=cuda)), "scale must be float32"),
+        (dict(scale=torch.ones((), dtype=torch.float32)), "scale must be a CUDA tensor"),
+        (dict(bias=torch.zeros(N, dtype=torch.bfloat16, device=cuda)), "bias must have the same dtype as c"),
+        (dict(bias=torch.zeros(64, dtype=torch.float16, device=cuda)), "bias must have N elements"),
+        (dict(a=misaligned), "a data pointer must be 16-byte aligned"),
+        (dict(cfg=(1, 1, 2, 8, 2)), r"M \(64\) must be divisible by kBlockM \(128\)"),
+        (dict(cfg=(1, 8, 4, 1, 2)), r"N \(128\) must be divisible by kBlockN \(256\)"),
+    ]
+    for change, msg in mutations:
+        y = good()
+        y.update(change)
+        assert not fast(y), msg
+        with pytest.raises(RuntimeError, match=msg):
+            hk.validate_scaled_mm(y["a"], y["b"], y["scale"], y["bias"], y["c"], *y["cfg"], y["b_dtype"])
+    # the any-M entry's relaxed rules: no block divisibility, bf16 activations
+    y = good()
+    y.update(cfg=(1, 1, 2, 8, 2), a=x["a"].bfloat16())
+    assert fast(y, block_divisible=False, allow_bf16_a=True)
+    assert not fast(y, block_divisible=True, allow_bf16_a=True)
+    assert not fast(y, block_divisible=False, allow_bf16_a=False)
