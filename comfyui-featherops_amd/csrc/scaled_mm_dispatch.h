@@ -49,10 +49,19 @@ enum KernelId : int {
 // have (bf16 activations are served by the split-K LDS tiles and the small-M
 // kernel with e5m2 weights only).
 bool launch_tile_kernel(int kernel_id, const MmArgs& p, hipStream_t stream);
+// K-split workspace layout, shared by the small-M kernel and the split-K LDS
+// tiles: a fixed region of arrival counters (one u32 per output strip or tile)
+// that nothing else ever writes, then the fp32 partials. The counter region
+// must be zero before the first call and every call leaves it zero again, so
+// one workspace serves calls of any shapes in any order (a counter region
+// sized per call would overlap an earlier call's partials). A split that would
+// need more counters than the region holds is not taken.
+constexpr int64_t kWorkspaceCounters = 16384;
+constexpr size_t kWorkspaceCounterBytes = static_cast<size_t>(kWorkspaceCounters) * 4;  // 64 KB
+
 // Small-M kernel. With a workspace of at least smallm_workspace_bytes() it
 // also splits K across workgroups; without one it splits K inside each
-// workgroup only. The workspace's first bytes are arrival counters that must
-// be zero before the first call; every call leaves them zero again.
+// workgroup only.
 bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups);
 int smallm_ksplit(int64_t M, int64_t N, int64_t K, int target_groups);
@@ -62,8 +71,8 @@ struct SplitKPlan {
     int kernel_id;          // 0: not applicable
     int ksplit;
     int tiles;
-    size_t counter_bytes;   // arrival counters (zero between calls), 256-byte padded
-    size_t workspace_bytes; // counters + ksplit fp32 partial tiles per output tile
+    size_t counter_bytes;   // the fixed counter region (kWorkspaceCounterBytes) when ksplit > 1
+    size_t workspace_bytes; // counter region + ksplit fp32 partial tiles per output tile
 };
 SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target);
 // Same workspace contract as launch_smallm_kernel.

@@ -497,7 +497,8 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     pl.kernel_id = bm == 32 ? kLdsSk32x128 : kLdsSk64x64;
     pl.ksplit = static_cast<int>(ks);
     pl.tiles = static_cast<int>(tiles);
-    pl.counter_bytes = ks > 1 ? (static_cast<size_t>(tiles) * 4 + 255) / 256 * 256 : 0;
+    if (tiles > kWorkspaceCounters) ks = 1;  // more tiles than the counter region holds
+    pl.counter_bytes = ks > 1 ? kWorkspaceCounterBytes : 0;
     pl.workspace_bytes = ks > 1 ? pl.counter_bytes + static_cast<size_t>(tiles) * ks * bm * bn * 4 : 0;
     return pl;
 }

@@ -315,11 +315,12 @@ SmallmPlan smallm_plan(int64_t M, int64_t N, int64_t K, int target_groups, bool 
     if (M <= 0 || M > 64) return pl;
     const int cus = target_groups > 0 ? target_groups : 256;
     if (mt >= kSplitMinMt) {
+        if (!allow_split) return pl;  // 16-column strips, K split inside the workgroup only
         pl.ct = ct_split(mt);
         const int64_t nstrips = (N + 16 * pl.ct - 1) / (16 * pl.ct);
         int64_t ks = (cus + nstrips - 1) / nstrips;
         if (ks > max_ks) ks = max_ks;
-        pl.ks = ks < 1 ? 1 : static_cast<int>(ks);
+        pl = ks > 1 ? SmallmPlan{pl.ct, static_cast<int>(ks)} : SmallmPlan{1, 1};
     } else {
         double best = smallm_cost_us(N, nst, 1, 1, cus);
         for (int ct : {1, 4})
@@ -331,6 +332,8 @@ SmallmPlan smallm_plan(int64_t M, int64_t N, int64_t K, int target_groups, bool 
                 }
             }
     }
+    if (pl.ks > 1 && (N + 16 * pl.ct - 1) / (16 * pl.ct) > kWorkspaceCounters)
+        return smallm_plan(M, N, K, target_groups, false);  // more strips than the counter region holds
 #ifdef FEATHER_SMALLM_PROBE
     if (const char* e = std::getenv("FEATHEROPS_SMALLM_CT")) pl.ct = std::atoi(e);
     if (const char* e = std::getenv("FEATHEROPS_SMALLM_KS")) pl.ks = std::atoi(e);
@@ -346,9 +349,8 @@ size_t smallm_workspace_bytes(int64_t M, int64_t N, int64_t K, int target_groups
     const SmallmPlan pl = smallm_plan(M, N, K, target_groups);
     if (pl.ks <= 1) return 0;
     const int64_t nstrips = (N + 16 * pl.ct - 1) / (16 * pl.ct);
-    // counters first (256-byte aligned), then ksplit partial tiles per strip
-    const size_t counter_bytes = (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256;
-    return counter_bytes + static_cast<size_t>(nstrips) * pl.ks * M * 16 * pl.ct * 4;
+    // the fixed counter region, then ksplit partial tiles per strip
+    return kWorkspaceCounterBytes + static_cast<size_t>(nstrips) * pl.ks * M * 16 * pl.ct * 4;
 }
 
 bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -361,13 +363,10 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
     if (pl.ks > 1 && (workspace == nullptr || workspace_bytes < smallm_workspace_bytes(p.M, p.N, p.K, target))) {
         // no (or too small a) workspace: split K inside each workgroup only
         pl = smallm_plan(p.M, p.N, p.K, target, false);
-        if (mt >= kSplitMinMt) pl = SmallmPlan{1, 1};
     }
     if (pl.ks > 1) {
-        const int64_t nstrips = (p.N + 16 * pl.ct - 1) / (16 * pl.ct);
         counters = static_cast<uint32_t*>(workspace);
-        partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                            (static_cast<size_t>(nstrips) * 4 + 255) / 256 * 256);
+        partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kWorkspaceCounterBytes);
     }
     const int ks = pl.ks;
     const bool wide = pl.ct >= 2;

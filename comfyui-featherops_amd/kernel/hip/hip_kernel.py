@@ -54,7 +54,9 @@ def _valid_fast(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, un
             and ((b_dtype == 1 and b_prepacked.dtype == torch.float8_e5m2)
                  or (b_dtype == 0 and b_prepacked.dtype == torch.float8_e4m3fn))
             and K % 16 == 0 and Kg == K // 16 and sixteen == 16 and tuple(c.shape) == (M, N)
-            and a.stride() == (K, 1) and b_prepacked.stride() == (N * 16, 16, 1) and c.stride() == (N, 1)
+            and (M == 1 or a.stride(0) == K) and a.stride(1) == 1
+            and (Kg == 1 or b_prepacked.stride(0) == N * 16) and b_prepacked.stride(1) == 16
+            and b_prepacked.stride(2) == 1 and (M == 1 or c.stride(0) == N) and c.stride(1) == 1
             and (scale is None or (scale.device == dev and scale.dtype == torch.float32 and scale.numel() == 1))
             and (bias is None or (bias.device == dev and bias.dtype == c.dtype and bias.numel() == N))
             and a.data_ptr() % 16 == 0 and b_prepacked.data_ptr() % 16 == 0 and c.data_ptr() % 16 == 0
@@ -99,12 +101,13 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     _check(b_prepacked.shape[2] == 16, "b_prepacked.shape[2] must be 16")
     _check(c.shape[0] == M, "c.shape[0] must equal M")
     _check(c.shape[1] == N, "c.shape[1] must equal N")
-    _check(a.stride(0) == K, f"a.stride(0) must equal K ({K})")
+    # (the stride of a dimension of size 1 is never used, so any value passes)
+    _check(M == 1 or a.stride(0) == K, f"a.stride(0) must equal K ({K})")
     _check(a.stride(1) == 1, "a.stride(1) must be 1")
-    _check(b_prepacked.stride(0) == N * 16, f"b_prepacked.stride(0) must equal N*16 ({N * 16})")
+    _check(K // 16 == 1 or b_prepacked.stride(0) == N * 16, f"b_prepacked.stride(0) must equal N*16 ({N * 16})")
     _check(b_prepacked.stride(1) == 16, "b_prepacked.stride(1) must be 16")
     _check(b_prepacked.stride(2) == 1, "b_prepacked.stride(2) must be 1")
-    _check(c.stride(0) == N, f"c.stride(0) must equal N ({N})")
+    _check(M == 1 or c.stride(0) == N, f"c.stride(0) must equal N ({N})")
     _check(c.stride(1) == 1, "c.stride(1) must be 1")
     if scale is not None:
         if require_cuda:
@@ -133,9 +136,10 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     _check(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit")
 
 
-# Per-(device, stream) workspaces for the small-M split-K kernel. They start
-# zero-filled and every call leaves their counter words zero again; keying by
-# stream keeps concurrent streams on separate workspaces.
+# Per-(device, stream) workspaces for the K-split kernels (small-M kernel and
+# split-K tiles). They start zero-filled and every call leaves their counter
+# region zero again, whatever the shape; keying by stream keeps concurrent
+# streams on separate workspaces.
 _WORKSPACES: dict = {}
 
 

@@ -67,10 +67,13 @@ bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* sc
  * (the reference ABI has no workspace, so launch_scaled_mm runs those shapes
  * without the cross-workgroup split). workspace_bytes must
  * be at least feather_scaled_mm_workspace_size(...) (0 means none needed; a
- * smaller workspace falls back to the unsplit kernel). The workspace must be
- * zero-filled before its first use and is left zero-filled by every call;
- * calls that run concurrently need distinct workspaces. No counterpart in the
- * reference; the torch op binding uses it.
+ * smaller workspace falls back to the unsplit kernel). Its first 64 KB hold
+ * arrival counters: they must be zero before the first use and every call
+ * leaves them zero; the rest is scratch for fp32 partial sums. One workspace
+ * (zero-filled once, sized for the largest call) therefore serves calls of
+ * any shapes in sequence on one stream; calls that run concurrently need
+ * distinct workspaces. No counterpart in the reference; the torch op binding
+ * uses it.
  */
 bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
                                  uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,

@@ -239,6 +239,35 @@ def test_small_m_split_k_workspace(cuda, M, N, K):
         assert (ws[: tiles * 4] == 0).all(), "arrival counters must be left at zero"
 
 
+def test_workspace_shared_across_shapes(cuda):
+    """One workspace, zeroed once, serves a sequence of K-split calls of
+    different shapes: a call with more tiles than the one before must not read
+    that call's leftover partials as arrival counters. Small-M kernel and
+    split-K LDS tiles, each shape twice, fewer tiles before more."""
+    from gpu_util import lib, stream
+
+    seq = [(16, 3072, 12288), (16, 5120, 13824), (1, 3072, 12288), (256, 1024, 1472), (512, 1072, 1024),
+           (64, 4096, 4096), (48, 12288, 2048), (16, 5120, 13824), (512, 1072, 1024)]
+    cfg = (2, 2, 4, 4, 4)
+    need = max(lib().feather_scaled_mm_workspace_size(M, N, K, *cfg) for M, N, K in seq)
+    ws = torch.zeros(need, dtype=torch.uint8, device=cuda)
+    for i, (M, N, K) in enumerate(seq):
+        g = torch.Generator().manual_seed(i)
+        a = torch.randn(M, K, generator=g).half()
+        packed, s = weight_like(N, K, g)
+        ref = O.scaled_mm_ref(a.numpy(), packed, s, None, O.DT_F16)
+        assert lib().feather_scaled_mm_workspace_size(M, N, K, *cfg) > 0, "every shape here splits K"
+        ad, bd, sd = a.to(cuda), to_dev_codes(packed, cuda), torch.tensor([s], device=cuda)
+        for rep in range(2):
+            c = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
+            assert lib().feather_launch_scaled_mm_ws(ad.data_ptr(), bd.data_ptr(), sd.data_ptr(), None, c.data_ptr(),
+                                                     M, N, K, 1, 0, *cfg, 1, 0, ws.data_ptr(), ws.numel(),
+                                                     stream(cuda))
+            torch.cuda.synchronize()
+            assert_gemm_close(c, ref, torch.float16, f"shared workspace step {i} {M}x{N}x{K} rep {rep}")
+        assert (ws[:65536] == 0).all(), "the counter region is left zero"
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (16, 12288, 512), (48, 1024, 2048), (64, 1024, 1024),
                                    (256, 768, 512), (1024, 4096, 1024), (100, 512, 1040)])
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
@@ -316,3 +345,24 @@ def test_validation_fast_path_matches_full(cuda, hk):
     assert fast(y, block_divisible=False, allow_bf16_a=True)
     assert not fast(y, block_divisible=True, allow_bf16_a=True)
     assert not fast(y, block_divisible=False, allow_bf16_a=False)
+
+
+def test_size_one_dims_any_stride(cuda, hk):
+    """A dimension of size 1 may carry any stride (torch leaves it arbitrary,
+    e.g. after .contiguous() of a permuted (1, N, 16) weight): M = 1
+    activations/outputs and K = 16 weights with odd size-1 strides run and
+    match the oracle."""
+    g = torch.Generator().manual_seed(21)
+    M, N, K = 1, 96, 16
+    a = torch.randn(M, K, generator=g).half()
+    packed, s = weight_like(N, K, g)
+    ref = O.scaled_mm_ref(a.numpy(), packed, s, None, O.DT_F16)
+    ad = a.to(cuda).as_strided((M, K), (999, 1))
+    bd = to_dev_codes(packed, cuda).as_strided((1, N, 16), (7, 16, 1))
+    assert ad.stride(0) != K and bd.stride(0) != N * 16
+    y = hk.scaled_mm_hip_any_m(ad, bd, torch.tensor(s, device=cuda), None, torch.float16)
+    torch.cuda.synchronize()
+    assert_gemm_close(y, ref, torch.float16, "size-1 strides any_m")
+    # the op's validation also accepts an M = 1 output with any row stride
+    c = torch.empty((1, N), dtype=torch.float16, device=cuda).as_strided((1, N), (5, 1))
+    hk.validate_scaled_mm(ad, bd, torch.tensor(s, device=cuda), None, c, 1, 1, 1, 1, 2, 1, block_divisible=False)

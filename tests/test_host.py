@@ -173,6 +173,6 @@ def test_small_m_plan_workspace(pkg):
     cfg = (1, 1, 2, 1, 2)
     assert lib.feather_scaled_mm_workspace_size(16, 4096, 4096, *cfg) == 0  # 256 strips: one per CU
     assert lib.feather_scaled_mm_workspace_size(16, 13824, 5120, *cfg) == 0  # 216 strips of 64 columns
-    # 80 strips of 64 columns x 3 K ranges: counters (256-aligned) + 3 fp32 partial tiles per strip
-    assert lib.feather_scaled_mm_workspace_size(16, 5120, 13824, *cfg) == 512 + 80 * 3 * 16 * 64 * 4
-    assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 256 + 48 * 4 * 1 * 64 * 4
+    # 80 strips of 64 columns x 3 K ranges: the fixed 64 KB counter region + 3 fp32 partial tiles per strip
+    assert lib.feather_scaled_mm_workspace_size(16, 5120, 13824, *cfg) == 65536 + 80 * 3 * 16 * 64 * 4
+    assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 65536 + 48 * 4 * 1 * 64 * 4
