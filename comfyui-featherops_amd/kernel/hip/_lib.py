@@ -70,8 +70,15 @@ def lib() -> ctypes.CDLL:
     return _handle
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
-    """Raw hipStream_t of torch's current stream on `device`."""
+    """Raw hipStream_t of torch's current stream on `device` (torch's direct
+    accessor: ~0.1 us against ~2 us for building a Stream object)."""
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
