@@ -66,4 +66,22 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint8_t*
         : "memory");
 }
 
+// As dma16, with the LDS destination given as a byte address in LDS (e.g. a
+// __shared__ array's address plus a constant): M0 is an operand of the asm,
+// so the compiler sets it (often to an immediate) and keeps no copy of it,
+// and no generic-to-LDS pointer conversion (with its null check) is needed.
+__device__ __forceinline__ void dma16_lds(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile(
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(sbase), "{m0}"(lds_addr)
+        : "memory");
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
 }  // namespace feather

@@ -132,25 +132,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         else if constexpr (b == 1) return sbuf1;
         else return sbuf2;
     };
+    // LDS byte address of stage buffer `tag` (a constant)
+    auto stage_lds = [&](auto tag) -> uint32_t { return lds_addr_of(stage_buf(tag)); };
     // copy i (A copies first, then B copies) of stage kt into buffer `tag`
     auto issue_one = [&](auto tag, int kt, int i) {
-        uint8_t* sa = stage_buf(tag);
+        const uint32_t la = stage_lds(tag);
         if (i < kAPerWave) {
-            dma16(a_base + kt * (kBK * 2), a_off[i], sa + ((i * kWaves + wave) * 8) * 128);
+            dma16_lds(a_base + kt * (kBK * 2), a_off[i], la + ((i * kWaves + wave) * 8) * 128);
         } else {
             const int j = i - kAPerWave;
-            dma16(b_base + kt * b_stage_bytes, b_off[j], sa + kAStage + (b_copy(j) * 64) * 16);
+            dma16_lds(b_base + kt * b_stage_bytes, b_off[j], la + kAStage + (b_copy(j) * 64) * 16);
         }
     };
     auto issue_stage = [&](auto tag, int kt) {
-        uint8_t* sa = stage_buf(tag);
-        uint8_t* sb = sa + kAStage;
-        const uint8_t* ab = a_base + kt * (kBK * 2);
-        const uint8_t* bb = b_base + kt * b_stage_bytes;
 #pragma unroll
-        for (int j = 0; j < kAPerWave; ++j) dma16(ab, a_off[j], sa + ((j * kWaves + wave) * 8) * 128);
-#pragma unroll
-        for (int j = 0; j < kBPerWave; ++j) dma16(bb, b_off[j], sb + (b_copy(j) * 64) * 16);
+        for (int i = 0; i < kLoadsPerStage; ++i) issue_one(tag, kt, i);
     };
     // LDS byte offset of this lane's A operand for M repeat rm, K half kh
     auto a_lds = [&](int rm, int kh) -> int {
@@ -233,22 +229,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         stage_barrier();
         read_b(S0{}, braw);
         read_a(S0{}, 0, araw[0]);
-        auto run_stage = [&](auto cur, int kt) {
+        // kFull: stages kt + 1 and kt + 2 exist (no bounds checks, so the
+        // steady-state loop body has no branches around the copies)
+        auto run_stage = [&](auto cur, auto full, int kt) {
             constexpr int c = decltype(cur)::value;
+            constexpr bool kFull = decltype(full)::value;
             using Next = std::integral_constant<int, (c + 1) % 3>;
             using Free = std::integral_constant<int, (c + 2) % 3>;  // stage kt + 2's buffer
+            const bool has2 = kFull || kt + 2 < nk;
+            const bool has1 = kFull || kt + 1 < nk;
             mm_half(0, araw[0], braw, [&](int rm) {
                 if (rm == 0) read_a(cur, 1, araw[1]);
 #pragma unroll
                 for (int i = 0; i < kLoadsPerStage; ++i)
-                    if (rm == (i * RM) / kLoadsPerStage && kt + 2 < nk) issue_one(Free{}, kt + 2, i);
+                    if (rm == (i * RM) / kLoadsPerStage && has2) issue_one(Free{}, kt + 2, i);
             });
             // mm_half widens braw before the first hook, so the hook may
             // overwrite braw with the next stage's operands
             mm_half(1, araw[1], braw, [&](int rm) {
-                if (rm == kBarrierRm && kt + 1 < nk) {
+                if (rm == kBarrierRm && has1) {
                     // this wave's reads of stage kt have returned, stage kt + 1 has landed
-                    if (kt + 2 < nk) wait_vmcnt_lgkm0<kLoadsPerStage>();
+                    if (has2) wait_vmcnt_lgkm0<kLoadsPerStage>();
                     else wait_vmcnt_lgkm0<0>();
                     stage_barrier();
                     read_b(Next{}, braw);
@@ -256,10 +257,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
                 }
             });
         };
-        for (int kt = 0; kt < nk; kt += 3) {
-            run_stage(S0{}, kt);
-            if (kt + 1 < nk) run_stage(S1{}, kt + 1);
-            if (kt + 2 < nk) run_stage(S2{}, kt + 2);
+        using Full = std::true_type;
+        using Tail = std::false_type;
+        int kt = 0;
+        for (; kt + 5 <= nk; kt += 3) {
+            run_stage(S0{}, Full{}, kt);
+            run_stage(S1{}, Full{}, kt + 1);
+            run_stage(S2{}, Full{}, kt + 2);
+        }
+        for (; kt < nk; kt += 3) {
+            run_stage(S0{}, Tail{}, kt);
+            if (kt + 1 < nk) run_stage(S1{}, Tail{}, kt + 1);
+            if (kt + 2 < nk) run_stage(S2{}, Tail{}, kt + 2);
         }
     } else {
         // Plain schedule: at the top of stage kt wait for its copies (issued
