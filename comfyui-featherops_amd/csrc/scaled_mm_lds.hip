@@ -19,11 +19,16 @@
 //   * per stage, the K halves are processed one after the other (all M
 //     repeats of K half 0, then of K half 1), so only half of the widened B
 //     operands are live at a time;
-//   * default schedule: LDS operands are read one K half ahead of the MFMAs
-//     that use them, the barrier sits early in each stage's second half, and
-//     copies are issued one at a time between MFMA groups (measured on the
-//     M=32768 K=5120 N=13824 shape: ~5% faster than barrier-at-the-top with
-//     burst-issued copies, which is kept as FEATHEROPS_LDS_PIPE=0);
+//   * default schedule: the barrier sits early in each stage's second half,
+//     after which the next stage's operands can be read while the current
+//     stage's remaining MFMAs run (measured on the M=32768 K=5120 N=13824
+//     shape: ~5% faster than barrier-at-the-top, which is kept as
+//     FEATHEROPS_LDS_PIPE=0). The source asks for A one K half ahead and the
+//     copies spread between MFMA groups; the compiler's scheduler keeps the
+//     kernel at 255 VGPRs by reading A about one M repeat ahead instead and
+//     issues each stage's copies together before the barrier (pinning the
+//     source order with scheduling barriers spills, and the other scheduler
+//     strategies measured 0-2.5% slower);
 //   * rows past M / columns past N are clamped to the last valid row/column
 //     (their results are computed and dropped), so every copy is in bounds.
 #include <stdlib.h>
@@ -206,16 +211,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     };
 
     if constexpr (kPipe == 1) {
-        // Operands one K half ahead. Register set araw[kh] holds the A
+        // Operands one K half ahead (as written; see the file header for what
+        // the scheduler makes of it). Register set araw[kh] holds the A
         // fragments of K half kh of the current stage: the second half's are
         // requested at the start of the first half's MFMAs. Stage kt + 2's
-        // copies go out one at a time between the first half's M repeats
-        // (a burst of them stalls instruction issue while the address unit
-        // drains it). Early in the second half -- once every wave has all of
-        // stage kt in registers -- a barrier publishes stage kt + 1 (its copies
-        // were waited for just before) and frees stage kt's buffer, and stage
-        // kt + 1's first-half operands are requested while the remaining
-        // repeats run.
+        // copies are placed between the first half's M repeats. Early in the
+        // second half -- once every wave has all of stage kt in registers --
+        // a barrier publishes stage kt + 1 (its copies were waited for just
+        // before) and frees stage kt's buffer, and stage kt + 1's first-half
+        // operands are requested while the remaining repeats run.
         constexpr int kBarrierRm = RM / 4;
         uint4 araw[2][RM];
         uint4 braw[RN];
