@@ -45,31 +45,15 @@ typedef __attribute__((address_space(3))) void lds_void;
 // (r & 7) ^ ((r >> 3) & 1) takes the conflict-free 4.
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// 16 bytes per lane from sbase + voff into LDS at lds_dst + 16 * lane
-// (sbase and lds_dst wave-uniform). Inline asm so that the compiler's
-// wait-count tracking does not treat the copy as an LDS write that every later
-// ds_read might alias (it would put a vmcnt(0) in front of the current stage's
-// reads, draining the copies of the next stages); the kernel waits with
-// explicit vmcnt counts instead. M0 is saved and restored around the copy.
-__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint8_t* lds_dst) {
-    const uint32_t lds_off =
-        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds_dst)));
-    uint32_t saved_m0;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved_m0)
-        : "v"(voff), "s"(sbase), "s"(lds_off)
-        : "memory");
-}
-
-// As dma16, with the LDS destination given as a byte address in LDS (e.g. a
-// __shared__ array's address plus a constant): M0 is an operand of the asm,
-// so the compiler sets it (often to an immediate) and keeps no copy of it,
-// and no generic-to-LDS pointer conversion (with its null check) is needed.
+// 16 bytes per lane from sbase + voff into LDS at lds_addr + 16 * lane
+// (sbase and lds_addr wave-uniform; lds_addr a byte address in LDS, e.g. a
+// __shared__ array's address plus a constant). Inline asm so that the
+// compiler's wait-count tracking does not treat the copy as an LDS write that
+// every later ds_read might alias (it would put a vmcnt(0) in front of the
+// current stage's reads, draining the copies of the next stages); the
+// kernels wait with explicit vmcnt counts instead. M0 is an operand of the
+// asm, so the compiler sets it (often to an immediate) and keeps no copy of
+// it, and no generic-to-LDS pointer conversion (with its null check) is needed.
 __device__ __forceinline__ void dma16_lds(const void* sbase, uint32_t voff, uint32_t lds_addr) {
     asm volatile(
         "s_nop 0\n\t"

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
             // Row r of a 16-row tile holds its 64-K stage as 8 chunks of 16
             // bytes, chunk c at position c ^ swz(r). Each wave uses its own
             // slab, so only this wave's copy count is waited for.
-            uint8_t* slab = smem + wave * (U * MT * kSlabTile);
+            const uint32_t slab = lds_addr_of(smem) + wave * (U * MT * kSlabTile);
             if (base > st_begin + wave) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): last slab reads done
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -109,8 +109,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
                             const int row = mt * 16 + r16 < M ? mt * 16 + r16 : M - 1;
                             int c = (lane & 7) ^ swz(r16);
                             if (st * 4 + (c >> 1) >= kgroups) c = 0;  // past K: any in-row chunk (zeroed below)
-                            dma16(A, (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + st * 64 + c * 8) * 2u,
-                                  slab + (u * MT + mt) * kSlabTile + j * 1024);
+                            dma16_lds(A, (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + st * 64 + c * 8) * 2u,
+                                      slab + (u * MT + mt) * kSlabTile + j * 1024);
                         }
                     }
                 }
