@@ -21,8 +21,6 @@
 //     counter for the next call. Partials and counters use device-coherent
 //     (agent-scope) loads, stores and atomics; the splits of a strip are also
 //     placed on one XCD (workgroup p runs on XCD p % 8).
-#include <cstdlib>
-
 #include "feather_common.h"
 #include "lds_dma.h"
 #include "scaled_mm_dispatch.h"
@@ -334,10 +332,6 @@ SmallmPlan smallm_plan(int64_t M, int64_t N, int64_t K, int target_groups, bool 
     }
     if (pl.ks > 1 && (N + 16 * pl.ct - 1) / (16 * pl.ct) > kWorkspaceCounters)
         return smallm_plan(M, N, K, target_groups, false);  // more strips than the counter region holds
-#ifdef FEATHER_SMALLM_PROBE
-    if (const char* e = std::getenv("FEATHEROPS_SMALLM_CT")) pl.ct = std::atoi(e);
-    if (const char* e = std::getenv("FEATHEROPS_SMALLM_KS")) pl.ks = std::atoi(e);
-#endif
     return pl;
 }
 
