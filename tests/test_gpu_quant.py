@@ -226,3 +226,23 @@ def test_config5_weight_on_device(cuda, quant):
     codes_nk = quant.unprepack_transpose(qdata)[rows]
     ref = O.e5m2_encode(w[rows].float().cpu().numpy() * (np.float32(1.0) / np.float32(scale.item())))
     assert np.array_equal(_bytes(codes_nk), ref)
+
+
+def test_capi_quantize_workspace_reused_across_shapes(cuda):
+    """feather_quantize_prepack_e5m2 through the C ABI with one 1 KB workspace
+    reused across weights of different sizes (different numbers of partial
+    maxima): codes and scale bit-exact against the oracle each time."""
+    ws = torch.full((256,), -1, dtype=torch.int32, device=cuda)  # garbage: no clearing needed
+    for i, (N, K) in enumerate([(4096, 4096), (7, 48), (3072, 1024), (1, 16), (640, 2048)]):
+        g = torch.Generator().manual_seed(40 + i)
+        w = (torch.randn(N, K, generator=g) * 0.05).half()
+        out = torch.empty(K // 16, N, 16, dtype=torch.uint8, device=cuda)
+        scale = torch.empty((), dtype=torch.float32, device=cuda)
+        wd = w.to(cuda)
+        st = lib().feather_quantize_prepack_e5m2(wd.data_ptr(), 0, N, K, None, 1, out.data_ptr(), scale.data_ptr(),
+                                                 ws.data_ptr(), stream(cuda))
+        assert st == 0
+        torch.cuda.synchronize()
+        codes, s_ref = O.quantize_native(w.numpy(), O.DT_F16)
+        assert np.float32(scale.item()) == s_ref, f"{N}x{K}"
+        assert np.array_equal(O.unprepack_transpose(out.cpu().numpy()), codes), f"{N}x{K}"
