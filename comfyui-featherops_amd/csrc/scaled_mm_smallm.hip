@@ -236,8 +236,9 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
 }
 
 // Shape policy for M > 32 (measured on MI355X, weights rotated past the
-// MALL): strips of 32 columns, K split across workgroups up to the workgroup
-// target. For M <= 32 see smallm_plan's cost model.
+// MALL): strips of 32 columns with K split across workgroups up to the
+// workgroup target, or 16-column strips when K is too short to split (or no
+// workspace is given). For M <= 32 see smallm_plan's cost model.
 constexpr int kSplitMinMt = 3;
 constexpr int ct_split(int mt) { return mt <= 2 ? 4 : 2; }
 
