@@ -158,11 +158,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         const int row = wave_m * WTM + rm * 16 + lr;
         return row * 128 + (((2 * lg + kh) ^ swz(row)) << 4);
     };
+    // operand reads as LDS byte addresses: a constant per buffer (and M / N
+    // repeat) plus one per-lane offset, so the constants can sit in the
+    // ds_read offset field instead of in extra address registers
+    auto lds_ld16 = [](uint32_t addr) -> uint4 {
+        using v4 = uint32_t __attribute__((ext_vector_type(4)));
+        const v4 v = *reinterpret_cast<const __attribute__((address_space(3))) v4*>(static_cast<uintptr_t>(addr));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    const uint32_t b_lane = static_cast<uint32_t>((lg * BN + wave_n * WTN + lr) * 16);
+    const uint32_t a_lane0 = static_cast<uint32_t>(a_lds(0, 0));
+    const uint32_t a_lane1 = static_cast<uint32_t>(a_lds(0, 1));
     auto read_b = [&](auto cur, uint4 (&braw)[RN]) {
-        const uint8_t* sb = stage_buf(cur) + kAStage;
+        const uint32_t sb = stage_lds(cur) + kAStage + b_lane;
 #pragma unroll
-        for (int rn = 0; rn < RN; ++rn)
-            braw[rn] = *reinterpret_cast<const uint4*>(sb + (lg * BN + wave_n * WTN + rn * 16 + lr) * 16);
+        for (int rn = 0; rn < RN; ++rn) braw[rn] = lds_ld16(sb + rn * 256);
     };
 
     f32x4 acc[RM][RN];
@@ -176,10 +186,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     using S2 = std::integral_constant<int, 2>;
 
     // A fragments of one K half of a stage, for every M repeat
+    // (the A swizzle depends on row & 15 only, so M repeat rm adds rm * 16 rows)
     auto read_a = [&](auto tag, int kh, uint4 (&dst)[RM]) {
-        const uint8_t* sa = stage_buf(tag);
+        const uint32_t sa = stage_lds(tag) + (kh ? a_lane1 : a_lane0);
 #pragma unroll
-        for (int rm = 0; rm < RM; ++rm) dst[rm] = *reinterpret_cast<const uint4*>(sa + a_lds(rm, kh));
+        for (int rm = 0; rm < RM; ++rm) dst[rm] = lds_ld16(sa + rm * 16 * 128);
     };
     // MFMAs of one K half: widen this half of the B operands, then run every
     // M repeat; `hook(rm)` runs before the MFMAs of repeat rm. The widened
