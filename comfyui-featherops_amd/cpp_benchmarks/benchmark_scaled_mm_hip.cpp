@@ -12,6 +12,9 @@
 // buffers so that a weight larger than the 256 MB Infinity Cache in total is
 // streamed from HBM), --b e5m2|e4m3. Default config is the gfx950 256x256
 // tile (2,4,4,8,4).
+// --quant: time feather_quantize_prepack_e5m2 on an N x K fp16 weight instead
+// (amax pass + quantize/prepack pass, 5 bytes per element of algorithmic
+// traffic: 2 read for the amax, 2 read + 1 written for the codes).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -47,12 +50,13 @@ struct Opts {
     int out_bf16 = 0;
     int b_dtype = FEATHER_B_E5M2;
     int rotate = 1;
+    bool quant = false;
 };
 
 void usage(const char* argv0) {
     std::cout << "Usage: " << argv0
               << " [--m M] [--n N] [--k K] [--warmup W] [--iters I] [--warps_m M] [--warps_n N] [--unroll U]"
-                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R]\n";
+                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant]\n";
 }
 
 Opts parse(int argc, char** argv) {
@@ -79,6 +83,7 @@ Opts parse(int argc, char** argv) {
         else if (a == "--out") o.out_bf16 = val() == "bf16";
         else if (a == "--b") o.b_dtype = val() == "e4m3" ? FEATHER_B_E4M3FN : FEATHER_B_E5M2;
         else if (a == "--rotate") o.rotate = std::max(1, std::stoi(val()));
+        else if (a == "--quant") o.quant = true;
         else if (a == "--help" || a == "-h") {
             usage(argv[0]);
             std::exit(0);
@@ -102,10 +107,66 @@ uint16_t to_half_bits(float f) {
     return b;
 }
 
+// Quantize + prepack of an N x K fp16 weight with a computed per-tensor scale
+// (the load path of the reference's quant.py:52-74 with no checkpoint scale).
+int run_quant(const Opts& o) {
+    const size_t nw = static_cast<size_t>(o.n) * o.k;
+    std::mt19937 gen(42);
+    std::normal_distribution<float> nrm(0.f, 0.02f);
+    std::vector<uint16_t> hw(nw);
+    for (auto& x : hw) x = to_half_bits(nrm(gen));
+    std::vector<void*> dw(o.rotate);
+    for (auto& p : dw) {
+        HIP_OK(hipMalloc(&p, nw * 2));
+        HIP_OK(hipMemcpy(p, hw.data(), nw * 2, hipMemcpyHostToDevice));
+    }
+    uint8_t* dq;
+    float* dscale;
+    uint32_t* dws;
+    HIP_OK(hipMalloc(&dq, nw));
+    HIP_OK(hipMalloc(&dscale, sizeof(float)));
+    HIP_OK(hipMalloc(&dws, 1024));
+    hipStream_t stream;
+    hipEvent_t t0, t1;
+    HIP_OK(hipStreamCreate(&stream));
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+    auto run = [&](int i) {
+        const int rc = feather_quantize_prepack_e5m2(dw[i % o.rotate], FEATHER_DTYPE_F16, o.n, o.k, nullptr, 0, dq,
+                                                     dscale, dws, stream);
+        if (rc != FEATHER_OK) {
+            std::cerr << "quantize failed: " << feather_status_string(rc) << std::endl;
+            std::exit(1);
+        }
+    };
+    for (int i = 0; i < o.warmup; ++i) run(i);
+    HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipEventRecord(t0, stream));
+    for (int i = 0; i < o.iters; ++i) run(i);
+    HIP_OK(hipEventRecord(t1, stream));
+    HIP_OK(hipEventSynchronize(t1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+    ms /= o.iters;
+    const double bytes = 5.0 * static_cast<double>(nw);
+    std::cout << std::fixed << std::setprecision(4);
+    std::cout << "quantize_prepack_e5m2 benchmark\n  problem: n=" << o.n << " k=" << o.k << " fp16 rotate=" << o.rotate
+              << "\n  back-to-back ms: " << ms << "  (GB/s " << bytes / ms / 1e6 << " on 5 B/element)" << std::endl;
+    for (auto p : dw) HIP_OK(hipFree(p));
+    HIP_OK(hipFree(dq));
+    HIP_OK(hipFree(dscale));
+    HIP_OK(hipFree(dws));
+    HIP_OK(hipEventDestroy(t0));
+    HIP_OK(hipEventDestroy(t1));
+    HIP_OK(hipStreamDestroy(stream));
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     const Opts o = parse(argc, argv);
+    if (o.quant) return run_quant(o);
     if (o.k % (16 * o.u) != 0) {
         std::cerr << "K must be divisible by 16 * unroll_k (" << 16 * o.u << ")" << std::endl;
         return 1;
