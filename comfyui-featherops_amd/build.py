@@ -1,10 +1,14 @@
-"""Build recipe for libfeatherops_amd.so (gfx950) and the C++ bench harnesses.
+"""Build recipe for libfeatherops_amd.so (gfx950), the torch op library and the
+C++ bench harnesses.
 
-Plain hipcc invocations, no torch involved: every `csrc/*.hip` file is
-compiled to an object in `_build/`, then linked into `lib/libfeatherops_amd.so`.
-The C++ benches in `cpp_benchmarks/` link against that library (mirroring the
-reference's cpp_benchmarks/build_benchmark_scaled_mm_hip.sh, which links the
-kernel's extern "C" ABI directly).
+Plain hipcc invocations: every `csrc/*.hip` file is compiled to an object in
+`_build/`, then linked into `lib/libfeatherops_amd.so` (no torch involved).
+`csrc/torch_op.cpp` (host C++ only) is compiled with g++ against torch's
+headers into `lib/libfeather_torch_ops.so`, which registers
+torch.ops.feather_ops.scaled_mm and links the library above.
+The C++ benches in `cpp_benchmarks/` link against libfeatherops_amd.so
+(mirroring the reference's cpp_benchmarks/build_benchmark_scaled_mm_hip.sh,
+which links the kernel's extern "C" ABI directly).
 
     python build.py            # library + benches
 """
@@ -25,6 +29,7 @@ INCLUDE = REPO_DIR / "include"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libfeatherops_amd.so"
+OPS_LIB_PATH = LIB_DIR / "libfeather_torch_ops.so"
 BENCH_DIR = PKG_DIR / "cpp_benchmarks"
 BENCH_BIN_DIR = BENCH_DIR / "build"
 
@@ -81,6 +86,26 @@ def build_library(jobs: int = 8) -> Path:
     return LIB_PATH
 
 
+def build_torch_ops() -> Path:
+    """lib/libfeather_torch_ops.so from csrc/torch_op.cpp (needs libfeatherops_amd.so)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}"]
+    cmd += [f"-I{p}" for p in cpp_extension.include_paths()]
+    cmd += [f"-I{rocm}/include", f"-I{INCLUDE}", str(CSRC / "torch_op.cpp"),
+            f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch",
+            f"-L{LIB_DIR}", "-lfeatherops_amd", "-Wl,-rpath,$ORIGIN"]
+    tmp = OPS_LIB_PATH.with_suffix(".so.tmp")
+    _run([*cmd, "-o", str(tmp)])
+    os.replace(tmp, OPS_LIB_PATH)
+    return OPS_LIB_PATH
+
+
 def build_benches() -> list[Path]:
     hipcc = _hipcc()
     BENCH_BIN_DIR.mkdir(exist_ok=True)
@@ -95,9 +120,12 @@ def build_benches() -> list[Path]:
 
 def build_all() -> None:
     build_library()
-    build_benches()
+    with ThreadPoolExecutor(max_workers=2) as ex:
+        jobs = [ex.submit(build_torch_ops), ex.submit(build_benches)]
+        for j in jobs:
+            j.result()
 
 
 if __name__ == "__main__":
     build_all()
-    print(f"built {LIB_PATH}")
+    print(f"built {LIB_PATH} and {OPS_LIB_PATH}")

@@ -1,0 +1,218 @@
+// torch ops of the library, registered in C++ so that an eager call goes from
+// torch's dispatcher straight to the launch entry without a Python frame:
+//   feather_ops::scaled_mm        the reference's op (kernel/hip/hip_kernel.cu:
+//                                 746-767: same namespace, schema, CUDA key)
+//   feather_ops::scaled_mm_any_m  any M, shape-picked tile, fp16/bf16 A (no
+//                                 counterpart in the reference; Meta kernel for
+//                                 fake tensors)
+//
+// Checks and messages follow the reference's scaled_mm (hip_kernel.cu:648-730);
+// the stride of a dimension of size 1 is never read, so any value passes.
+// Launches go to torch's current HIP stream of a's device. The K-split kernels
+// get a per-(device, stream) workspace: zero-filled when first allocated, and
+// left with its counter region zero by every call, whatever the shape.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "featherops_amd.h"
+
+namespace {
+
+at::Tensor& workspace_for(const at::Device& dev, hipStream_t stream, size_t nbytes) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, at::Tensor> pool;
+    std::lock_guard<std::mutex> lock(mu);
+    at::Tensor& ws = pool[{dev.index(), stream}];
+    if (!ws.defined() || static_cast<size_t>(ws.numel()) < nbytes) {
+        const int64_t n = static_cast<int64_t>(nbytes > (size_t(1) << 20) ? nbytes : (size_t(1) << 20));
+        ws = at::zeros({n}, at::TensorOptions().dtype(at::kByte).device(dev));
+    }
+    return ws;
+}
+
+// Argument checks of the reference's scaled_mm (hip_kernel.cu:648-730).
+// `block_divisible = false` replaces the BlockM/BlockN/ChunkK divisibility
+// rules by what the gfx950 kernels need (N % 16 == 0; K % 16 is always
+// required) and `allow_bf16_a` accepts bf16 activations: the any-M entry.
+void check_args(const at::Tensor& a, const at::Tensor& b_prepacked, const std::optional<at::Tensor>& scale,
+                const std::optional<at::Tensor>& bias, const at::Tensor& c, int64_t block_warps_m,
+                int64_t block_warps_n, int64_t unroll_k, int64_t repeat_m, int64_t repeat_n, int64_t b_dtype,
+                bool block_divisible, bool allow_bf16_a) {
+    TORCH_CHECK(a.is_cuda(), "a must be a CUDA tensor");
+    TORCH_CHECK(b_prepacked.is_cuda(), "b_prepacked must be a CUDA tensor");
+    TORCH_CHECK(c.is_cuda(), "c must be a CUDA tensor");
+    TORCH_CHECK(b_prepacked.device() == a.device(), "b_prepacked must be on the same device as a");
+    TORCH_CHECK(c.device() == a.device(), "c must be on the same device as a");
+    if (allow_bf16_a) {
+        TORCH_CHECK(a.scalar_type() == at::kHalf || a.scalar_type() == at::kBFloat16, "a must be float16 or bfloat16");
+    } else {
+        TORCH_CHECK(a.scalar_type() == at::kHalf, "a must be float16");
+    }
+    TORCH_CHECK(c.scalar_type() == at::kHalf || c.scalar_type() == at::kBFloat16, "c must be float16 or bfloat16");
+    TORCH_CHECK(b_dtype == 0 || b_dtype == 1, "b_dtype must be 0 (fp8e4m3) or 1 (fp8e5m2)");
+    if (b_dtype == 0) {
+        TORCH_CHECK(b_prepacked.scalar_type() == at::kFloat8_e4m3fn, "b_prepacked must be float8_e4m3fn when b_dtype=0");
+    } else {
+        TORCH_CHECK(b_prepacked.scalar_type() == at::kFloat8_e5m2, "b_prepacked must be float8_e5m2 when b_dtype=1");
+    }
+    TORCH_CHECK(a.dim() == 2, "a must be 2D");
+    TORCH_CHECK(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)");
+    TORCH_CHECK(c.dim() == 2, "c must be 2D");
+    const int64_t M = a.size(0), K = a.size(1), N = b_prepacked.size(1);
+    TORCH_CHECK(K % 16 == 0, "K must be divisible by 16");
+    TORCH_CHECK(b_prepacked.size(0) == K / 16, "b_prepacked.shape[0] must equal K/16 (", K / 16, ")");
+    TORCH_CHECK(b_prepacked.size(2) == 16, "b_prepacked.shape[2] must be 16");
+    TORCH_CHECK(c.size(0) == M, "c.shape[0] must equal M");
+    TORCH_CHECK(c.size(1) == N, "c.shape[1] must equal N");
+    TORCH_CHECK(M == 1 || a.stride(0) == K, "a.stride(0) must equal K (", K, ")");
+    TORCH_CHECK(a.stride(1) == 1, "a.stride(1) must be 1");
+    TORCH_CHECK(K / 16 == 1 || b_prepacked.stride(0) == N * 16, "b_prepacked.stride(0) must equal N*16 (", N * 16, ")");
+    TORCH_CHECK(b_prepacked.stride(1) == 16, "b_prepacked.stride(1) must be 16");
+    TORCH_CHECK(b_prepacked.stride(2) == 1, "b_prepacked.stride(2) must be 1");
+    TORCH_CHECK(M == 1 || c.stride(0) == N, "c.stride(0) must equal N (", N, ")");
+    TORCH_CHECK(c.stride(1) == 1, "c.stride(1) must be 1");
+    if (scale.has_value()) {
+        TORCH_CHECK(scale->is_cuda(), "scale must be a CUDA tensor");
+        TORCH_CHECK(scale->device() == a.device(), "scale must be on the same device as a");
+        TORCH_CHECK(scale->scalar_type() == at::kFloat, "scale must be float32");
+        TORCH_CHECK(scale->numel() == 1, "scale must have one element");
+    }
+    if (bias.has_value()) {
+        TORCH_CHECK(bias->is_cuda(), "bias must be a CUDA tensor");
+        TORCH_CHECK(bias->device() == a.device(), "bias must be on the same device as a");
+        TORCH_CHECK(bias->scalar_type() == c.scalar_type(), "bias must have the same dtype as c");
+        TORCH_CHECK(bias->numel() == N, "bias must have N elements");
+    }
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(a.data_ptr()) % 16 == 0, "a data pointer must be 16-byte aligned");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(b_prepacked.data_ptr()) % 16 == 0,
+                "b_prepacked data pointer must be 16-byte aligned");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(c.data_ptr()) % 16 == 0, "c data pointer must be 16-byte aligned");
+    const int64_t block_m = 16 * block_warps_m * repeat_m;
+    const int64_t block_n = 16 * block_warps_n * repeat_n;
+    const int64_t chunk_k = 16 * unroll_k;
+    if (block_divisible) {
+        TORCH_CHECK(block_m > 0 && M % block_m == 0, "M (", M, ") must be divisible by kBlockM (", block_m, ")");
+        TORCH_CHECK(block_n > 0 && N % block_n == 0, "N (", N, ") must be divisible by kBlockN (", block_n, ")");
+        TORCH_CHECK(chunk_k > 0 && K % chunk_k == 0, "K (", K, ") must be divisible by kChunkK (", chunk_k, ")");
+    } else {
+        TORCH_CHECK(N % 16 == 0, "N (", N, ") must be divisible by 16");
+    }
+    TORCH_CHECK(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit");
+}
+
+struct Launch {
+    const at::Tensor& b_prepacked;
+    const std::optional<at::Tensor>& scale;
+    const std::optional<at::Tensor>& bias;
+    const at::Tensor& c;
+    int64_t M, N, K;
+    int cfg[5];
+    int b_dtype;
+    void* ws;
+    size_t ws_size;
+    hipStream_t stream;
+
+    bool operator()(const at::Tensor& a, int a_dtype) const {
+        return feather_launch_scaled_mm_ex(
+            a.data_ptr(), a_dtype, static_cast<const uint8_t*>(b_prepacked.data_ptr()),
+            scale.has_value() ? static_cast<const float*>(scale->data_ptr()) : nullptr,
+            bias.has_value() ? static_cast<const uint16_t*>(bias->data_ptr()) : nullptr,
+            static_cast<uint16_t*>(c.data_ptr()), M, N, K, scale.has_value() ? 1 : 0, bias.has_value() ? 1 : 0,
+            cfg[0], cfg[1], cfg[2], cfg[3], cfg[4], b_dtype, c.scalar_type() == at::kHalf ? 0 : 1, ws, ws_size,
+            stream);
+    }
+};
+
+// Enqueue the GEMM for config `cfg` on torch's current stream of a's device
+// (the caller holds a device guard for it).
+Launch make_launch(const at::Tensor& a, const at::Tensor& b_prepacked, const std::optional<at::Tensor>& scale,
+                   const std::optional<at::Tensor>& bias, const at::Tensor& c, const int (&cfg)[5], int b_dtype) {
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(a.device().index()).stream();
+    const int64_t M = a.size(0), K = a.size(1), N = b_prepacked.size(1);
+    Launch l{b_prepacked, scale, bias, c, M, N, K, {cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]}, b_dtype, nullptr, 0,
+             stream};
+    const size_t ws_bytes = feather_scaled_mm_workspace_size(M, N, K, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]);
+    if (ws_bytes) {
+        at::Tensor& t = workspace_for(a.device(), stream, ws_bytes);
+        l.ws = t.data_ptr();
+        l.ws_size = static_cast<size_t>(t.numel());
+    }
+    return l;
+}
+
+// feather_ops::scaled_mm (hip_kernel.cu:648-743): writes c for the given config.
+void scaled_mm(const at::Tensor& a, const at::Tensor& b_prepacked, const std::optional<at::Tensor>& scale,
+               const std::optional<at::Tensor>& bias, const at::Tensor& c, int64_t block_warps_m,
+               int64_t block_warps_n, int64_t unroll_k, int64_t repeat_m, int64_t repeat_n, int64_t b_dtype) {
+    check_args(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
+               true, false);
+    const c10::DeviceGuard guard(a.device());
+    const int cfg[5] = {static_cast<int>(block_warps_m), static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
+                        static_cast<int>(repeat_m), static_cast<int>(repeat_n)};
+    TORCH_CHECK(make_launch(a, b_prepacked, scale, bias, c, cfg, static_cast<int>(b_dtype))(a, FEATHER_DTYPE_F16),
+                "Unsupported config");
+}
+
+// feather_ops::scaled_mm_any_m: any row count M without padding (the kernels
+// mask rows past M), the tile from feather_scaled_mm_pick_config, fp16 or bf16
+// activations. bf16 activations are rounded to fp16 inside the kernel where it
+// has that variant, otherwise by the library's round-to-nearest-even cast
+// first: the values of x.to(float16) (comfy_feather/ops.py:88) either way.
+at::Tensor scaled_mm_any_m(const at::Tensor& a, const at::Tensor& b_prepacked, const std::optional<at::Tensor>& scale,
+                           const std::optional<at::Tensor>& bias, at::ScalarType out_dtype) {
+    TORCH_CHECK(a.dim() == 2, "a must be 2D");
+    TORCH_CHECK(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)");
+    const int64_t M = a.size(0), K = a.size(1), N = b_prepacked.size(1);
+    at::Tensor c = at::empty({M, N}, a.options().dtype(out_dtype));
+    if (M == 0) return c;
+    const c10::DeviceGuard guard(a.device());
+    int cfg[5];
+    const int status = feather_scaled_mm_pick_config(M, N, K, cfg);
+    TORCH_CHECK(status == FEATHER_OK, "feather_scaled_mm_pick_config failed: ", feather_status_string(status));
+    const int b_dtype = b_prepacked.scalar_type() == at::kFloat8_e4m3fn ? 0 : 1;
+    check_args(a, b_prepacked, scale, bias, c, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4], b_dtype, false, true);
+    const Launch launch = make_launch(a, b_prepacked, scale, bias, c, cfg, b_dtype);
+    bool launched;
+    if (a.scalar_type() == at::kBFloat16) {
+        launched = launch(a, FEATHER_DTYPE_BF16);
+        if (!launched) {
+            const at::Tensor a16 = at::empty(a.sizes(), a.options().dtype(at::kHalf));
+            const int st = feather_bf16_to_fp16_rne(static_cast<const uint16_t*>(a.data_ptr()),
+                                                   static_cast<uint16_t*>(a16.data_ptr()), a.numel(), launch.stream);
+            TORCH_CHECK(st == FEATHER_OK, "feather_bf16_to_fp16_rne failed: ", feather_status_string(st));
+            launched = launch(a16, FEATHER_DTYPE_F16);
+        }
+    } else {
+        launched = launch(a, FEATHER_DTYPE_F16);
+    }
+    TORCH_CHECK(launched, "Unsupported config");
+    return c;
+}
+
+at::Tensor scaled_mm_any_m_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
+                                const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
+                                at::ScalarType out_dtype) {
+    return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
+}
+
+}  // namespace
+
+TORCH_LIBRARY(feather_ops, m) {
+    m.def("scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, int block_warps_m, "
+          "int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype) -> ()");
+    m.def("scaled_mm_any_m(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
+    m.impl("scaled_mm", &scaled_mm);
+    m.impl("scaled_mm_any_m", &scaled_mm_any_m);
+}
+
+TORCH_LIBRARY_IMPL(feather_ops, Meta, m) { m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta); }

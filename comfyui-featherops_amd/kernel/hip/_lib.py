@@ -13,6 +13,8 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "lib" / "libfeatherops_amd.so"
+# torch op library: feather_ops::scaled_mm registered in C++ over the same C ABI
+OPS_LIB_PATH = LIB_PATH.with_name("libfeather_torch_ops.so")
 
 FEATHER_OK = 0
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
@@ -45,7 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "feather_abi_version": (_int, []),
 }
 
-_lock = threading.Lock()
+_lock = threading.RLock()  # load_torch_ops loads the C library while holding it
 _handle: ctypes.CDLL | None = None
 
 
@@ -68,6 +70,26 @@ def lib() -> ctypes.CDLL:
                 fn.argtypes = args
             _handle = h
     return _handle
+
+
+_ops_loaded = False
+
+
+def load_torch_ops() -> None:
+    """Register torch.ops.feather_ops.scaled_mm from the C++ op library (once)."""
+    global _ops_loaded
+    if _ops_loaded:
+        return
+    with _lock:
+        if not _ops_loaded:
+            if not OPS_LIB_PATH.exists():
+                raise RuntimeError(
+                    f"FeatherOps torch op library not found at {OPS_LIB_PATH}; build it with "
+                    "`python comfyui-featherops_amd/build.py` (there is no non-HIP fallback)"
+                )
+            lib()  # the op library resolves the launch entry from libfeatherops_amd.so
+            torch.ops.load_library(str(OPS_LIB_PATH))
+            _ops_loaded = True
 
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)

@@ -10,8 +10,10 @@ Public names and signatures are the reference's:
 plus the native op `torch.ops.feather_ops.scaled_mm` with the reference
 schema (hip_kernel.cu:746-767) and its validation (hip_kernel.cu:648-730).
 
-The native op calls `launch_scaled_mm` of libfeatherops_amd.so through
-ctypes on torch's current stream; there is no other compute path.
+The native op is registered in C++ (csrc/torch_op.cpp, built into
+lib/libfeather_torch_ops.so) and calls libfeatherops_amd.so's launch entry on
+torch's current stream; the any-M op calls the library through ctypes. There
+is no other compute path.
 """
 
 from __future__ import annotations
@@ -136,72 +138,11 @@ def validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warp
     _check(32 * block_warps_m * block_warps_n <= 1024, "Block size exceeds HIP thread-per-block limit")
 
 
-# Per-(device, stream) workspaces for the K-split kernels (small-M kernel and
-# split-K tiles). They start zero-filled and every call leaves their counter
-# region zero again, whatever the shape; keying by stream keeps concurrent
-# streams on separate workspaces.
-_WORKSPACES: dict = {}
-
-
-def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (dev.index, stream)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
-    return ws
-
-
-class _NoSwitch:
-    def __enter__(self):
-        return None
-
-    def __exit__(self, *exc):
-        return False
-
-
-_NO_SWITCH = _NoSwitch()
-
-
-def _on_device(dev: torch.device):
-    """torch.cuda.device(dev) unless dev is already the current device."""
-    return _NO_SWITCH if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
-
-
-def _scaled_mm_native(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
-                      b_dtype) -> None:
-    validate_scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
-                       b_dtype)
-    L = _lib.lib()
-    dev = a.device
-    M, K = a.shape
-    N = b_prepacked.shape[1]
-    # the launch goes to the current HIP device: switch only when a lives elsewhere
-    with _on_device(dev):
-        stream = _lib.stream_ptr(dev)
-        ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m,
-                                                      repeat_n)
-        ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
-        launched = L.feather_launch_scaled_mm_ws(
-            a.data_ptr(), b_prepacked.data_ptr(),
-            scale.data_ptr() if scale is not None else None,
-            bias.data_ptr() if bias is not None else None,
-            c.data_ptr(), M, N, K,
-            1 if scale is not None else 0, 1 if bias is not None else 0,
-            block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
-            0 if c.dtype == torch.float16 else 1,
-            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
-    _check(bool(launched), "Unsupported config")
-
-
-# torch op feather_ops::scaled_mm with the reference schema (hip_kernel.cu:746-767)
-_SCHEMA = ("scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, "
-           "int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype) -> ()")
-if not hasattr(torch.ops, "feather_ops") or not hasattr(torch.ops.feather_ops, "scaled_mm"):
-    _LIB_DEF = torch.library.Library("feather_ops", "DEF")
-    _LIB_DEF.define(_SCHEMA)
-    _LIB_CUDA = torch.library.Library("feather_ops", "IMPL", "CUDA")
-    _LIB_CUDA.impl("scaled_mm", _scaled_mm_native)
+# torch op feather_ops::scaled_mm with the reference schema (hip_kernel.cu:746-767),
+# registered in C++ by lib/libfeather_torch_ops.so (csrc/torch_op.cpp): the same
+# checks and messages as validate_scaled_mm, then feather_launch_scaled_mm_ws on
+# torch's current stream with a per-(device, stream) workspace.
+_lib.load_torch_ops()
 
 
 def kernel_id(M: int, N: int, K: int, cfg) -> int:
@@ -328,7 +269,8 @@ def scaled_mm_hip(
 
 # The any-M entry's configuration: the library's shape-based pick
 # (feather_scaled_mm_pick_config: the output tile whose waves x tile cost is
-# smallest on this device), cached per shape and device.
+# smallest on this device), cached per shape and device. The op itself asks
+# the library for the same pick on every call.
 _PICKED: dict = {}
 
 
@@ -350,56 +292,10 @@ def any_m_config(M: int, N: int, K: int, device: torch.device | None = None) -> 
     return cfg
 
 
-@torch.library.custom_op("feather_ops_internal::scaled_mm_any_m", mutates_args=())
-def _any_m_op(
-    a: torch.Tensor,
-    b_prepacked: torch.Tensor,
-    scale: torch.Tensor | None,
-    bias: torch.Tensor | None,
-    out_dtype: torch.dtype,
-) -> torch.Tensor:
-    M, K = a.shape
-    N = b_prepacked.shape[1]
-    out = torch.empty((M, N), device=a.device, dtype=out_dtype)
-    if M == 0:
-        return out
-    cfg = any_m_config(M, N, K, a.device)
-    b_dtype = 0 if b_prepacked.dtype == torch.float8_e4m3fn else 1
-    validate_scaled_mm(a, b_prepacked, scale, bias, out, *cfg, b_dtype, block_divisible=False, allow_bf16_a=True)
-    L = _lib.lib()
-    dev = a.device
-    with _on_device(dev):
-        stream = _lib.stream_ptr(dev)
-        ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
-        ws = _workspace(dev, stream, ws_bytes) if ws_bytes else None
-
-        def launch(x, a_code):
-            return L.feather_launch_scaled_mm_ex(
-                x.data_ptr(), a_code, b_prepacked.data_ptr(), scale.data_ptr() if scale is not None else None,
-                bias.data_ptr() if bias is not None else None, out.data_ptr(), M, N, K,
-                1 if scale is not None else 0, 1 if bias is not None else 0, *cfg, b_dtype,
-                0 if out_dtype == torch.float16 else 1,
-                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
-
-        if a.dtype == torch.bfloat16:
-            # bf16 activations are rounded to fp16 inside the kernel where it has
-            # that variant; otherwise converted here first by the library's
-            # round-to-nearest cast (the values of ops.py:88's x.to(float16))
-            launched = launch(a, _lib.DTYPE_CODES[torch.bfloat16])
-            if not launched:
-                a16 = torch.empty(a.shape, dtype=torch.float16, device=dev)
-                _lib.check(L.feather_bf16_to_fp16_rne(a.data_ptr(), a16.data_ptr(), a.numel(), stream),
-                           "feather_bf16_to_fp16_rne")
-                launched = launch(a16, _lib.DTYPE_CODES[torch.float16])
-        else:
-            launched = launch(a, _lib.DTYPE_CODES[torch.float16])
-    _check(bool(launched), "Unsupported config")
-    return out
-
-
-@_any_m_op.register_fake
-def _(a, b_prepacked, scale, bias, out_dtype):
-    return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+# torch.ops.feather_ops.scaled_mm_any_m, registered in C++ with the native op
+# (csrc/torch_op.cpp): checks as validate_scaled_mm(block_divisible=False,
+# allow_bf16_a=True), the any_m_config tile, a Meta kernel for fake tensors.
+_any_m_op = torch.ops.feather_ops.scaled_mm_any_m.default
 
 
 def scaled_mm_hip_any_m(a, b_prepacked, scale, bias, out_dtype) -> torch.Tensor:
@@ -408,7 +304,7 @@ def scaled_mm_hip_any_m(a, b_prepacked, scale, bias, out_dtype) -> torch.Tensor:
     padding M to a block multiple, calling scaled_mm_hip and slicing. `a` may
     also be bf16: it is then rounded to fp16 (round to nearest even) inside the
     GEMM, the same values as calling it with a.to(torch.float16)."""
-    return _any_m_op(a, b_prepacked, scale, bias, out_dtype)
+    return torch.ops.feather_ops.scaled_mm_any_m.default(a, b_prepacked, scale, bias, out_dtype)
 
 
 def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:

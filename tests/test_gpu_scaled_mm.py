@@ -339,6 +339,10 @@ def test_validation_fast_path_matches_full(cuda, hk):
         assert not fast(y), msg
         with pytest.raises(RuntimeError, match=msg):
             hk.validate_scaled_mm(y["a"], y["b"], y["scale"], y["bias"], y["c"], *y["cfg"], y["b_dtype"])
+        # the C++ op (csrc/torch_op.cpp) raises the same message before launching anything
+        with pytest.raises(RuntimeError, match=msg):
+            torch.ops.feather_ops.scaled_mm.default(y["a"], y["b"], y["scale"], y["bias"], y["c"], *y["cfg"],
+                                                    y["b_dtype"])
     # the any-M entry's relaxed rules: no block divisibility, bf16 activations
     y = good()
     y.update(cfg=(1, 1, 2, 8, 2), a=x["a"].bfloat16())

@@ -144,8 +144,54 @@ def test_cpu_tensors_raise_loudly(hk):
     # the op has only a GPU kernel: CPU tensors hit torch's "no kernel for backend" error
     with pytest.raises((RuntimeError, NotImplementedError), match="CUDA"):
         torch.ops.feather_ops.scaled_mm.default(a, b, s, bias, c, 1, 1, 2, 1, 2, 1)
-    with pytest.raises(RuntimeError, match="CUDA tensor"):
-        hk._scaled_mm_native(a, b, s, bias, c, 1, 1, 2, 1, 2, 1)
+
+
+def test_native_op_registered_in_cpp(hk):
+    """torch.ops.feather_ops.scaled_mm comes from the C++ op library with the
+    reference's schema (hip_kernel.cu:746-767) and only a CUDA kernel."""
+    from featherops_amd.kernel.hip import _lib
+
+    assert _lib.OPS_LIB_PATH.exists()
+    op = torch.ops.feather_ops.scaled_mm.default
+    assert str(op._schema) == (
+        "feather_ops::scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, "
+        "int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype) -> ()")
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "CUDA")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "CPU")
+    # registered from a shared library, not from Python
+    assert "csrc/torch_op.cpp" in torch._C._dispatch_dump(op.name())
+    anym = torch.ops.feather_ops.scaled_mm_any_m.default
+    assert str(anym._schema) == ("feather_ops::scaled_mm_any_m(Tensor a, Tensor b_prepacked, Tensor? scale, "
+                                 "Tensor? bias, ScalarType out_dtype) -> Tensor")
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(anym.name(), "CUDA")
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(anym.name(), "Meta")
+    assert "csrc/torch_op.cpp" in torch._C._dispatch_dump(anym.name())
+
+
+def test_op_library_loads_first_in_fresh_process():
+    """Importing the op module before anything else has loaded the C library
+    (a fresh interpreter) registers the ops without blocking."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parents[1]
+    code = ("import sys; sys.path.insert(0, %r); import __graft_entry__ as g; g.load_package(); "
+            "import featherops_amd.kernel.hip.hip_kernel, torch; "
+            "print(torch.ops.feather_ops.scaled_mm_any_m.default.name())") % str(repo)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "feather_ops::scaled_mm_any_m" in r.stdout
+
+
+def test_any_m_fake_shapes(hk):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        a = torch.empty(37, 256, dtype=torch.bfloat16)
+        b = torch.empty(16, 128, 16, dtype=torch.float8_e5m2)
+        out = hk.scaled_mm_hip_any_m(a, b, None, None, torch.float16)
+        assert out.shape == (37, 128) and out.dtype == torch.float16
 
 
 def test_fake_impl_shapes_for_compile(hk):
