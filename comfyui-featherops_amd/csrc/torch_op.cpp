@@ -5,6 +5,9 @@
 //   feather_ops::scaled_mm_any_m  any M, shape-picked tile, fp16/bf16 A (no
 //                                 counterpart in the reference; Meta kernel for
 //                                 fake tensors)
+//   feather_ops_internal::scaled_mm_configured
+//                                 the reference's configured op (hip_kernel.py:
+//                                 12-58, a Python custom op there), Meta kernel
 //
 // Checks and messages follow the reference's scaled_mm (hip_kernel.cu:648-730);
 // the stride of a dimension of size 1 is never read, so any value passes.
@@ -196,6 +199,27 @@ at::Tensor scaled_mm_any_m(const at::Tensor& a, const at::Tensor& b_prepacked, c
     return c;
 }
 
+// feather_ops_internal::scaled_mm_configured (reference kernel/hip/hip_kernel.py:
+// 12-39): allocates C (M, N) of out_dtype and runs feather_ops::scaled_mm with
+// the weight dtype's code (e4m3fn -> 0, otherwise 1).
+at::Tensor scaled_mm_configured(const at::Tensor& a, const at::Tensor& b_prepacked,
+                                const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
+                                at::ScalarType out_dtype, int64_t block_warps_m, int64_t block_warps_n,
+                                int64_t unroll_k, int64_t repeat_m, int64_t repeat_n) {
+    TORCH_CHECK(a.dim() == 2, "a must be 2D");
+    TORCH_CHECK(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)");
+    at::Tensor c = at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
+    scaled_mm(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
+              b_prepacked.scalar_type() == at::kFloat8_e4m3fn ? 0 : 1);
+    return c;
+}
+
+at::Tensor scaled_mm_configured_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
+                                     const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
+                                     at::ScalarType out_dtype, int64_t, int64_t, int64_t, int64_t, int64_t) {
+    return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
+}
+
 at::Tensor scaled_mm_any_m_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
                                 const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
                                 at::ScalarType out_dtype) {
@@ -216,3 +240,14 @@ TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, Meta, m) { m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta); }
+
+// the reference's Python custom op of this name, as a C++ op (the namespace
+// also holds the Python-defined autotuned op, so this is a fragment)
+TORCH_LIBRARY_FRAGMENT(feather_ops_internal, m) {
+    m.def("scaled_mm_configured(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype, "
+          "int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(feather_ops_internal, CUDA, m) { m.impl("scaled_mm_configured", &scaled_mm_configured); }
+
+TORCH_LIBRARY_IMPL(feather_ops_internal, Meta, m) { m.impl("scaled_mm_configured", &scaled_mm_configured_meta); }

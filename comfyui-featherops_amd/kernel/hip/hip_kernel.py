@@ -155,32 +155,11 @@ def kernel_id(M: int, N: int, K: int, cfg) -> int:
 # ---------------------------------------------------------------------------
 
 
-@torch.library.custom_op("feather_ops_internal::scaled_mm_configured", mutates_args=())
-def _configured_op(
-    a: torch.Tensor,
-    b_prepacked: torch.Tensor,
-    scale: torch.Tensor | None,
-    bias: torch.Tensor | None,
-    out_dtype: torch.dtype,
-    block_warps_m: int,
-    block_warps_n: int,
-    unroll_k: int,
-    repeat_m: int,
-    repeat_n: int,
-) -> torch.Tensor:
-    out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
-    torch.ops.feather_ops.scaled_mm.default(
-        a, b_prepacked, scale, bias, out, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n,
-        0 if b_prepacked.dtype == torch.float8_e4m3fn else 1,
-    )
-    return out
-
-
-@_configured_op.register_fake
-def _(a, b_prepacked, scale, bias, out_dtype, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n):
-    return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
-
-
+# feather_ops_internal::scaled_mm_configured (hip_kernel.py:12-58) is registered
+# in C++ with the native op (csrc/torch_op.cpp), with a Meta kernel for fake
+# tensors: (a, b_prepacked, scale, bias, out_dtype, block_warps_m, block_warps_n,
+# unroll_k, repeat_m, repeat_n) -> C of out_dtype.
+_configured_op = torch.ops.feather_ops_internal.scaled_mm_configured.default
 scaled_mm_hip_configured = _configured_op
 
 # Reference configurations (hip_kernel.py:60-89), then four gfx950 tiles:

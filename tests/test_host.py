@@ -166,6 +166,13 @@ def test_native_op_registered_in_cpp(hk):
     assert torch._C._dispatch_has_kernel_for_dispatch_key(anym.name(), "CUDA")
     assert torch._C._dispatch_has_kernel_for_dispatch_key(anym.name(), "Meta")
     assert "csrc/torch_op.cpp" in torch._C._dispatch_dump(anym.name())
+    cfg = torch.ops.feather_ops_internal.scaled_mm_configured.default
+    assert str(cfg._schema) == (
+        "feather_ops_internal::scaled_mm_configured(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, "
+        "ScalarType out_dtype, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n) "
+        "-> Tensor")
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(cfg.name(), "Meta")
+    assert hk.scaled_mm_hip_configured is cfg
 
 
 def test_op_library_loads_first_in_fresh_process():
