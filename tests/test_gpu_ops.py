@@ -112,6 +112,55 @@ def test_torch_compile_configured_and_autotuned(cuda, hk):
     assert_gemm_close(y, ref2, torch.float16, "compile autotuned view input no scale")
 
 
+def test_torch_compile_any_m(cuda, hk):
+    """The any-M op (C++, Meta kernel for tracing) under torch.compile with
+    fullgraph: bf16 activations of a ragged M, the op traced as one call."""
+    g = torch.Generator().manual_seed(5)
+    K, N = 512, 384
+    b = torch.randn(K, N, generator=g).to(torch.float8_e5m2)
+    bp = hk.prepack_b_for_scaled_mm(b.to(cuda))
+    s = torch.tensor(0.75, device=cuda)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).to(cuda)
+
+    @torch.compile(fullgraph=True)
+    def f(x, bp, s, bias):
+        return hk.scaled_mm_hip_any_m(x.view(-1, x.shape[-1]), bp, s, bias, torch.bfloat16)
+
+    for m in (37, 300):
+        x = torch.randn(1, m, K, generator=g).to(torch.bfloat16).to(cuda)
+        y = f(x, bp, s, bias)
+        assert y.shape == (m, N) and y.dtype == torch.bfloat16
+        ref = O.scaled_mm_ref(x.view(m, K).to(torch.float16).cpu().numpy(), bp.view(torch.uint8).cpu().numpy(),
+                              np.float32(0.75), bias.cpu().view(torch.int16).numpy().view(np.uint16), O.DT_BF16)
+        assert_gemm_close(y, ref, torch.bfloat16, f"compile any-M {m}")
+
+
+def test_two_streams_keep_separate_workspaces(cuda, hk):
+    """K-split calls (small-M kernel, workspace from the C++ op's per-stream
+    pool) issued on two streams at once give the single-stream results."""
+    g = torch.Generator(device=cuda).manual_seed(11)
+    K, N = 8192, 1024
+    b = (torch.randn(K, N, generator=g, device=cuda) * 0.02).to(torch.float8_e5m2)
+    bp = hk.prepack_b_for_scaled_mm(b)
+    s = torch.tensor(2.0, device=cuda)
+    xs = [torch.randn(m, K, generator=g, device=cuda).half() for m in (16, 24, 8, 32)]
+    for x in xs:  # every call takes the K split across workgroups
+        assert hk._lib.lib().feather_scaled_mm_workspace_size(x.shape[0], N, K, *hk.any_m_config(x.shape[0], N, K)) > 0
+    want = [hk.scaled_mm_hip_any_m(x, bp, s, None, torch.float16) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    got = [None] * len(xs)
+    for rep in range(3):
+        for i, x in enumerate(xs):
+            with torch.cuda.stream(streams[i % 2]):
+                got[i] = hk.scaled_mm_hip_any_m(x, bp, s, None, torch.float16)
+        torch.cuda.synchronize()
+        for i in range(len(xs)):
+            assert torch.equal(got[i], want[i]), f"rep {rep} call {i}"
+
+
 def test_graph_capture_replays_match_eager(cuda, hk, quant):
     """scaled_mm (small-M kernel with and without its K split, split-K tiles,
     bf16 activations) and quantize captured in a HIP graph: every replay, with
