@@ -24,8 +24,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel.hip.hip_kernel import scaled_mm_hip, scaled_mm_hip_any_m
-from .lora import apply_lora_patches
+from ..kernel.hip.hip_kernel import scaled_mm_hip, scaled_mm_hip_any_m, scaled_mm_hip_any_m_lora
+from .lora import apply_lora_patches, lora_factors
 from .quant import (
     HAVE_COMFY,
     get_feather_plain_tensors,
@@ -94,6 +94,7 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
 
         class Linear(manual_cast.Linear):
             pad_m = False
+            fuse_lora = True
 
             def __init__(self, *args, **kwargs):
                 super().__init__(*args, **kwargs)
@@ -145,7 +146,7 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                 assert inplace_update is False
                 _set_weight(self, weight)
 
-            def _forward_padded(self, x):
+            def _forward_padded(self, x, lora=None):
                 dtype_orig = x.dtype
                 x = x.contiguous()
                 if self.pad_m or x.dtype != torch.bfloat16:
@@ -162,6 +163,8 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                 scale = scale.to(device=x.device, dtype=torch.float32)
                 if self.pad_m:
                     y = scaled_mm_hip(x, weight, scale, bias, out_dtype=self.out_dtype)
+                elif lora is not None:
+                    y = scaled_mm_hip_any_m_lora(x, weight, scale, bias, self.out_dtype, *lora)
                 else:
                     y = scaled_mm_hip_any_m(x, weight, scale, bias, self.out_dtype)
                 uncast_bias_weight(self, weight, bias, offload_stream)
@@ -188,9 +191,13 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                     m_padded = (m + block - 1) // block * block
                     x_padded = F.pad(x, (0, 0, 0, m_padded - m)) if m_padded != m else x
                     y = self._forward_padded(x_padded)[:m]
+                    y = apply_lora_patches(x, y, self.weight_function)
                 else:
-                    y = self._forward_padded(x)
-                y = apply_lora_patches(x, y, self.weight_function)
+                    # basic LoRA patches go into the GEMM's epilogue (one pass over C)
+                    lora = lora_factors(x, self.weight_function) if self.fuse_lora else None
+                    y = self._forward_padded(x, lora)
+                    if lora is None:
+                        y = apply_lora_patches(x, y, self.weight_function)
                 return y.view(*shape[:-1], y.shape[-1])
 
     return FeatherOps

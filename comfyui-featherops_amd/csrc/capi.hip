@@ -179,6 +179,42 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
     return feather::launch_tile_kernel(kid, p, stream);
 }
 
+bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                                   uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                                   const uint16_t* lora_t, const uint16_t* lora_u, int64_t rank, int lora_dtype,
+                                   int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                   int b_dtype, int output_dtype, hipStream_t stream) {
+    const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    // the rank-R epilogue exists on the large LDS tiles (fp16 activations, e5m2 weights)
+    if (kid < feather::kLds256x256w2x4 || is_splitk(kid)) return false;
+    if (b_dtype != FEATHER_B_E5M2 || (output_dtype != 0 && output_dtype != 1)) return false;
+    if (lora_dtype != FEATHER_DTYPE_F16 && lora_dtype != FEATHER_DTYPE_BF16) return false;
+    if (lora_t == nullptr || lora_u == nullptr || rank <= 0 || rank % 32 != 0 || rank > INT32_MAX / 2) return false;
+    if ((reinterpret_cast<uintptr_t>(lora_t) | reinterpret_cast<uintptr_t>(lora_u)) % 16 != 0) return false;
+    if (M == 0) return true;
+    feather::MmArgs p;
+    p.a = static_cast<const uint16_t*>(a);
+    p.b = b_prepacked;
+    p.scale = scale;
+    p.bias = bias;
+    p.c = c;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.has_scale = has_scale ? 1 : 0;
+    p.has_bias = has_bias ? 1 : 0;
+    p.out_bf16 = output_dtype == 1;
+    p.b_e4m3 = false;
+    p.a_bf16 = false;
+    p.group_m = tuning_group_m();
+    p.smallm_min_groups = tuning_smallm_groups();
+    p.lora_t = lora_t;
+    p.lora_u = lora_u;
+    p.lora_rank = rank;
+    p.lora_dtype = lora_dtype == FEATHER_DTYPE_F16 ? 1 : 2;
+    return feather::launch_lds_kernel(kid, p, stream);
+}
+
 bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
                                  uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
                                  int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,

@@ -172,4 +172,11 @@ __device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// The same shape on bf16 operands (8 bf16 values per lane in each uint4).
+__device__ __forceinline__ f32x4 mfma16x16x32_bf16(uint4 a, uint4 b, f32x4 c) {
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
 }  // namespace feather

@@ -20,6 +20,11 @@ struct MmArgs {
     bool a_bf16;             // activations are bf16 (converted to fp16 in the kernel; e5m2 weights only)
     int group_m;             // tile raster group height (0 = default)
     int smallm_min_groups;   // small-M: workgroup count the K split aims for (0 = default)
+    // rank-R epilogue update C += T . U^T (LDS tiles only): T (M, R), U (N, R)
+    const uint16_t* lora_t = nullptr;
+    const uint16_t* lora_u = nullptr;
+    int64_t lora_rank = 0;
+    int lora_dtype = 0;      // 0 none, 1 fp16 factors, 2 bf16 factors
 };
 
 // Kernel variants. Values are stable: the Python autotuner de-duplicates

@@ -30,7 +30,13 @@
 //     source order with scheduling barriers spills, and the other scheduler
 //     strategies measured 0-2.5% slower);
 //   * rows past M / columns past N are clamped to the last valid row/column
-//     (their results are computed and dropped), so every copy is in bounds.
+//     (their results are computed and dropped), so every copy is in bounds;
+//   * optional rank-R update in the epilogue (kLora, the unmerged LoRA side
+//     path of the reference's comfy_feather/lora.py:4-35): after the weight
+//     scale, acc += T(M x R) . U(N x R)^T on the fp16 or bf16 MFMA, from
+//     fragments read straight from global memory (both factors are small and
+//     shared by many tiles), before the rounding to the output type. The
+//     separate pass that would re-read and re-write C disappears.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -45,11 +51,14 @@ namespace {
 constexpr int kBK = 64;
 
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, bool kABf16>
+// kLora: 0 = none, 1 = fp16 factors, 2 = bf16 factors (T is M x R, U is N x R,
+// both row-major with R % 32 == 0 and 16-byte aligned rows)
+template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, bool kABf16, int kLora>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
-    int tiles_m, int tiles_n, int group_m, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters) {
+    int tiles_m, int tiles_n, int group_m, int ksplit, float* __restrict__ partials, uint32_t* __restrict__ counters,
+    const uint16_t* __restrict__ lora_t, const uint16_t* __restrict__ lora_u, int lora_rank) {
     constexpr int kWaves = WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M;
     constexpr int WTN = BN / WAVES_N;
@@ -375,6 +384,44 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             __hip_atomic_store(&counters[lin], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
+    if constexpr (kLora != 0) {
+        // the weight scale applies to the fp8 product only: scale first, then
+        // add the rank-R term in fp32 (one MFMA K step per 32 ranks; weights'
+        // role for U, activations' role for T, so the accumulator layout is
+        // the main loop's)
+#pragma unroll
+        for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+            for (int rn = 0; rn < RN; ++rn)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[rm][rn][i] = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
+        const int trow0 = m0 + wave_m * WTM + lr;
+        const int ucol0 = n0 + wave_n * WTN + lr;
+        for (int r0 = 0; r0 < lora_rank; r0 += 32) {
+            uint4 tf[RM], uf[RN];
+#pragma unroll
+            for (int rm = 0; rm < RM; ++rm) {
+                const int row = trow0 + rm * 16 < M ? trow0 + rm * 16 : M - 1;
+                tf[rm] = *reinterpret_cast<const uint4*>(lora_t + static_cast<int64_t>(row) * lora_rank + r0 + 8 * lg);
+            }
+#pragma unroll
+            for (int rn = 0; rn < RN; ++rn) {
+                const int col = ucol0 + rn * 16 < N ? ucol0 + rn * 16 : N - 1;
+                uf[rn] = *reinterpret_cast<const uint4*>(lora_u + static_cast<int64_t>(col) * lora_rank + r0 + 8 * lg);
+            }
+#pragma unroll
+            for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+                for (int rn = 0; rn < RN; ++rn) {
+                    if constexpr (kLora == 1)
+                        acc[rm][rn] = mfma16x16x32(as_half8(uf[rn]), as_half8(tf[rm]), acc[rm][rn]);
+                    else
+                        acc[rm][rn] = mfma16x16x32_bf16(uf[rn], tf[rm], acc[rm][rn]);
+                }
+        }
+    }
+
     // ---- epilogue: each wave stages its whole WTM x WTN output tile in LDS
     // (the stage buffers, free once every wave is past its last stage) with
     // one wait, then stores rows of WTN * 2 contiguous bytes ----
@@ -405,7 +452,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         for (int rn = 0; rn < RN; ++rn) {
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
+            for (int i = 0; i < 4; ++i)
+                v[i] = kLora != 0 ? acc[rm][rn][i]
+                                  : opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
             // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
             const int chunk = (2 * rn + (lg >> 1) + row) % kCPR;
             *reinterpret_cast<uint2*>(sc + row * kRowBytes + chunk * 16 + (lg & 1) * 8) =
@@ -437,11 +486,28 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
     const int group_m = p.group_m > 0 ? p.group_m : 4;
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
-#define FEATHER_LDS_LAUNCH(BF, E4, AB)                                                                                \
-    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, AB>), grid, block, 0, stream,    \
-                       p.a, p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),                  \
+#define FEATHER_LDS_LAUNCH_L(BF, E4, AB, LORA)                                                                        \
+    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, AB, LORA>), grid, block, 0,      \
+                       stream, p.a, p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),          \
                        static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, partials,   \
-                       counters)
+                       counters, p.lora_t, p.lora_u, static_cast<int>(p.lora_rank))
+#define FEATHER_LDS_LAUNCH(BF, E4, AB) FEATHER_LDS_LAUNCH_L(BF, E4, AB, 0)
+    if (p.lora_dtype != 0) {
+        // rank-R epilogue: the default schedule's large tiles, fp16 activations,
+        // e5m2 weights, no K split
+        if constexpr (PIPE == 1 && BM >= 128) {
+            if (p.a_bf16 || p.b_e4m3 || ksplit != 1) return false;
+            if (p.lora_dtype == 1) {
+                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, false, 1);
+                else FEATHER_LDS_LAUNCH_L(false, false, false, 1);
+            } else {
+                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, false, 2);
+                else FEATHER_LDS_LAUNCH_L(false, false, false, 2);
+            }
+            return true;
+        }
+        return false;
+    }
     if (p.a_bf16) {
         // bf16 activations: the small split-K tiles only (default schedule, e5m2
         // weights). On the large tiles, where every A fragment is read by 2-4
@@ -464,6 +530,7 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
         else FEATHER_LDS_LAUNCH(false, false, false);
     }
 #undef FEATHER_LDS_LAUNCH
+#undef FEATHER_LDS_LAUNCH_L
     return true;
 }
 
@@ -496,8 +563,8 @@ int lds_pipe_env() {
 
 bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
     if (p.K % kBK != 0) return false;
-    return lds_pipe_env() == 0 && !p.a_bf16 ? launch_lds_pipe<0>(kernel_id, p, stream)
-                                            : launch_lds_pipe<1>(kernel_id, p, stream);
+    return lds_pipe_env() == 0 && !p.a_bf16 && p.lora_dtype == 0 ? launch_lds_pipe<0>(kernel_id, p, stream)
+                                                                 : launch_lds_pipe<1>(kernel_id, p, stream);
 }
 
 // Split-K plan for M <= 64: a 32- or 64-row tile and enough K splits to give

@@ -5,6 +5,9 @@
 //   feather_ops::scaled_mm_any_m  any M, shape-picked tile, fp16/bf16 A (no
 //                                 counterpart in the reference; Meta kernel for
 //                                 fake tensors)
+//   feather_ops::scaled_mm_any_m_lora
+//                                 the any-M op plus an unmerged-LoRA term,
+//                                 fused into the epilogue on the large tiles
 //   feather_ops_internal::scaled_mm_configured
 //                                 the reference's configured op (hip_kernel.py:
 //                                 12-58, a Python custom op there), Meta kernel
@@ -220,6 +223,72 @@ at::Tensor scaled_mm_configured_meta(const at::Tensor& a, const at::Tensor& b_pr
     return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
 }
 
+// feather_ops::scaled_mm_any_m_lora: scaled_mm_any_m plus the unmerged-LoRA
+// term T . U^T (reference comfy_feather/lora.py:4-35, after F.linear(x, A);
+// the strengths are folded into T by the caller). T (M, R) and U (N, R) are
+// contiguous fp16 or bf16 with R % 32 == 0. On the large LDS tiles the term is
+// added to the scaled fp32 accumulator before rounding; on every other route
+// the GEMM runs as scaled_mm_any_m and the term is added to C afterwards.
+at::Tensor scaled_mm_any_m_lora(const at::Tensor& a, const at::Tensor& b_prepacked,
+                                const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
+                                at::ScalarType out_dtype, const at::Tensor& lora_t, const at::Tensor& lora_u) {
+    TORCH_CHECK(a.dim() == 2, "a must be 2D");
+    TORCH_CHECK(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)");
+    const int64_t M = a.size(0), K = a.size(1), N = b_prepacked.size(1);
+    TORCH_CHECK(lora_t.is_cuda() && lora_u.is_cuda() && lora_t.device() == a.device() && lora_u.device() == a.device(),
+                "lora_t and lora_u must be CUDA tensors on a's device");
+    TORCH_CHECK(lora_t.scalar_type() == lora_u.scalar_type() &&
+                    (lora_t.scalar_type() == at::kHalf || lora_t.scalar_type() == at::kBFloat16),
+                "lora_t and lora_u must both be float16 or both bfloat16");
+    TORCH_CHECK(lora_t.dim() == 2 && lora_u.dim() == 2 && lora_t.size(0) == M && lora_u.size(0) == N &&
+                    lora_t.size(1) == lora_u.size(1),
+                "lora_t must be (M, R) and lora_u (N, R)");
+    const int64_t R = lora_t.size(1);
+    TORCH_CHECK(R > 0 && R % 32 == 0, "lora rank must be a positive multiple of 32 (pad with zero columns)");
+    TORCH_CHECK(lora_t.is_contiguous() && lora_u.is_contiguous(), "lora_t and lora_u must be contiguous");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(lora_t.data_ptr()) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(lora_u.data_ptr()) % 16 == 0,
+                "lora_t and lora_u data pointers must be 16-byte aligned");
+    if (M == 0) return at::empty({M, N}, a.options().dtype(out_dtype));
+    const c10::DeviceGuard guard(a.device());
+    int cfg[5];
+    const int status = feather_scaled_mm_pick_config(M, N, K, cfg);
+    TORCH_CHECK(status == FEATHER_OK, "feather_scaled_mm_pick_config failed: ", feather_status_string(status));
+    const int b_dtype = b_prepacked.scalar_type() == at::kFloat8_e4m3fn ? 0 : 1;
+    const int kid = feather_scaled_mm_kernel_id(M, N, K, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]);
+    // the fused epilogue: large LDS tiles (kernel ids 20-29), e5m2 weights
+    if (kid >= 20 && kid < 30 && b_dtype == 1) {
+        at::Tensor c = at::empty({M, N}, a.options().dtype(out_dtype));
+        check_args(a, b_prepacked, scale, bias, c, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4], b_dtype, false, true);
+        const hipStream_t stream = c10::hip::getCurrentHIPStream(a.device().index()).stream();
+        at::Tensor a16 = a;
+        if (a.scalar_type() == at::kBFloat16) {  // the large tiles take fp16 activations
+            a16 = at::empty(a.sizes(), a.options().dtype(at::kHalf));
+            const int st = feather_bf16_to_fp16_rne(static_cast<const uint16_t*>(a.data_ptr()),
+                                                    static_cast<uint16_t*>(a16.data_ptr()), a.numel(), stream);
+            TORCH_CHECK(st == FEATHER_OK, "feather_bf16_to_fp16_rne failed: ", feather_status_string(st));
+        }
+        const bool launched = feather_launch_scaled_mm_lora(
+            a16.data_ptr(), static_cast<const uint8_t*>(b_prepacked.data_ptr()),
+            scale.has_value() ? static_cast<const float*>(scale->data_ptr()) : nullptr,
+            bias.has_value() ? static_cast<const uint16_t*>(bias->data_ptr()) : nullptr,
+            static_cast<uint16_t*>(c.data_ptr()), M, N, K, scale.has_value() ? 1 : 0, bias.has_value() ? 1 : 0,
+            static_cast<const uint16_t*>(lora_t.data_ptr()), static_cast<const uint16_t*>(lora_u.data_ptr()), R,
+            lora_t.scalar_type() == at::kHalf ? FEATHER_DTYPE_F16 : FEATHER_DTYPE_BF16, cfg[0], cfg[1], cfg[2],
+            cfg[3], cfg[4], b_dtype, out_dtype == at::kHalf ? 0 : 1, stream);
+        if (launched) return c;
+    }
+    at::Tensor c = scaled_mm_any_m(a, b_prepacked, scale, bias, out_dtype);
+    c.add_(at::mm(lora_t, lora_u.t()).to(out_dtype));
+    return c;
+}
+
+at::Tensor scaled_mm_any_m_lora_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
+                                     const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
+                                     at::ScalarType out_dtype, const at::Tensor& lora_t, const at::Tensor& lora_u) {
+    return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
+}
+
 at::Tensor scaled_mm_any_m_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
                                 const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
                                 at::ScalarType out_dtype) {
@@ -232,14 +301,20 @@ TORCH_LIBRARY(feather_ops, m) {
     m.def("scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, int block_warps_m, "
           "int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int b_dtype) -> ()");
     m.def("scaled_mm_any_m(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype) -> Tensor");
+    m.def("scaled_mm_any_m_lora(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype, "
+          "Tensor lora_t, Tensor lora_u) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm", &scaled_mm);
     m.impl("scaled_mm_any_m", &scaled_mm_any_m);
+    m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora);
 }
 
-TORCH_LIBRARY_IMPL(feather_ops, Meta, m) { m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta); }
+TORCH_LIBRARY_IMPL(feather_ops, Meta, m) {
+    m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta);
+    m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora_meta);
+}
 
 // the reference's Python custom op of this name, as a C++ op (the namespace
 // also holds the Python-defined autotuned op, so this is a fragment)

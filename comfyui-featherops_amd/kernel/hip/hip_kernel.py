@@ -286,6 +286,15 @@ def scaled_mm_hip_any_m(a, b_prepacked, scale, bias, out_dtype) -> torch.Tensor:
     return torch.ops.feather_ops.scaled_mm_any_m.default(a, b_prepacked, scale, bias, out_dtype)
 
 
+def scaled_mm_hip_any_m_lora(a, b_prepacked, scale, bias, out_dtype, lora_t, lora_u) -> torch.Tensor:
+    """scaled_mm_hip_any_m(...) + lora_t @ lora_u.T: the unmerged-LoRA term
+    (reference comfy_feather/lora.py:4-35) with the strengths folded into
+    lora_t (M, R); lora_u is (N, R); both contiguous fp16 or bf16, R % 32 == 0.
+    On the large tiles the term joins the fp32 accumulator before the output
+    rounding (no second pass over C); other routes add it to C afterwards."""
+    return torch.ops.feather_ops.scaled_mm_any_m_lora.default(a, b_prepacked, scale, bias, out_dtype, lora_t, lora_u)
+
+
 def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
     """(K, N) -> (K/16, N, 16) (hip_kernel.py:170-171), on the GPU.
 

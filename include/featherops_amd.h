@@ -103,6 +103,25 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
                                  hipStream_t stream);
 
 /*
+ * feather_launch_scaled_mm_ws with the unmerged-LoRA term fused into the
+ * epilogue: C = rnd(acc * scale + T . U^T) (+ bias in the output type), where
+ * T is (M, rank) and U is (N, rank), both row-major, 16-byte aligned, in
+ * lora_dtype (FEATHER_DTYPE_F16 or FEATHER_DTYPE_BF16), rank % 32 == 0 (pad
+ * with zero columns), and the LoRA strengths already folded into T. Replaces
+ * the separate y += F.linear(F.linear(x, A), B) * s of the reference's
+ * comfy_feather/lora.py:4-35 for the part after F.linear(x, A): the caller
+ * computes T = F.linear(x, A) * s. Served by the LDS-DMA tiles (K % 64 == 0,
+ * a routed tile of at least 128 x 128) with fp16 activations and e5m2
+ * weights; returns false and launches nothing otherwise (the caller then
+ * adds the term itself). Needs no workspace.
+ */
+bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                                   uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                                   const uint16_t* lora_t, const uint16_t* lora_u, int64_t rank, int lora_dtype,
+                                   int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                   int b_dtype, int output_dtype, hipStream_t stream);
+
+/*
  * A configuration tuple for this shape on the current device, without timing
  * anything: the output tile whose waves of workgroups times tile cost is
  * smallest (256x256, 256x192, 128x256, 256x128 or 128x128; the small-M

@@ -27,7 +27,9 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                     -> scale 1/65504, dequant error <= half a code step)
   scaled_mm_*       brute-force float64 loops on tiny shapes, all-ones weight
                     -> row sums, identity weight, naive == ref when no fp16
-                    overflow
+                    overflow; lora= : zero factors == no term, constant
+                    factors -> closed-form R*t*u added before the rounding
+                    (a term that moves a value across an fp16 tie)
 """
 
 from __future__ import annotations
@@ -268,12 +270,15 @@ def dequantize(codes_nk: np.ndarray, scale: float, dtype: str) -> np.ndarray:
 # ---------------------------------------------------------------------------
 
 
-def _finish(acc32: np.ndarray, scale, bias, out_dtype: str) -> np.ndarray:
-    """scale in fp32 -> round to out dtype -> bias added in out dtype."""
+def _finish(acc32: np.ndarray, scale, bias, out_dtype: str, term=None) -> np.ndarray:
+    """scale in fp32 -> (+ term, one fp32 rounding) -> round to out dtype ->
+    bias added in out dtype."""
     with np.errstate(over="ignore", invalid="ignore"):
         c = acc32.astype(np.float32)
         if scale is not None:
             c = c * np.float32(scale)
+        if term is not None:
+            c = (c.astype(np.float64) + term).astype(np.float32)
         if out_dtype == DT_F16:
             y = f32_to_fp16_rne(c)
             if bias is not None:
@@ -293,16 +298,27 @@ def _decode_b(b_prepacked: np.ndarray, b_dtype: str) -> np.ndarray:
 
 
 def scaled_mm_ref(a: np.ndarray, b_prepacked: np.ndarray, scale, bias, out_dtype: str,
-                  b_dtype: str = "e5m2") -> np.ndarray:
+                  b_dtype: str = "e5m2", lora=None) -> np.ndarray:
     """The kernel contract (hip_kernel.cu:366-419 with a round-to-nearest bf16
     epilogue): sum in float64 then float32, scale on the float32 value, round
     to the output type, add bias in the output type. fp16 out -> float16 array,
-    bf16 out -> uint16 bits."""
+    bf16 out -> uint16 bits.
+
+    lora=(T, U): the fused unmerged-LoRA epilogue -- T (M, R) . U (N, R)^T,
+    summed in float64, is added to the scaled float32 value before the output
+    rounding. This is the build's own contract for that path: the reference
+    (comfy_feather/lora.py:4-35) instead adds F.linear(F.linear(x, A), B) * s
+    to the finished output with a rounding to x's dtype after every step, so
+    the two agree to those roundings, not bit for bit."""
     a64 = np.asarray(a, dtype=np.float16).astype(np.float64)
     b64 = _decode_b(b_prepacked, b_dtype).astype(np.float64)
     with np.errstate(over="ignore", invalid="ignore"):
         acc = (a64 @ b64).astype(np.float32)
-    return _finish(acc, scale, bias, out_dtype)
+    term = None
+    if lora is not None:
+        t, u = (np.asarray(f, dtype=np.float64) for f in lora)
+        term = t @ u.T
+    return _finish(acc, scale, bias, out_dtype, term)
 
 
 def scaled_mm_ref_f32(a: np.ndarray, b_prepacked: np.ndarray, scale, b_dtype: str = "e5m2") -> np.ndarray:

@@ -205,6 +205,28 @@ def test_scaled_mm_oracle_special_weights():
     assert np.array_equal(yn, yr)
 
 
+def test_scaled_mm_oracle_lora_term():
+    """lora=(T, U) adds T . U^T to the scaled float32 value before the output
+    rounding: zero factors change nothing; constant factors give R*t*u, placed
+    so that only the before-rounding order moves the result across an fp16 tie."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((8, 64)).astype(np.float16)
+    b = O.prepack_kn(rng.integers(0x30, 0x3C, (64, 32), dtype=np.uint8))
+    z_t, z_u = np.zeros((8, 32)), np.zeros((32, 32))
+    for od in (O.DT_F16, O.DT_BF16):
+        assert np.array_equal(O.scaled_mm_ref(a, b, np.float32(0.5), None, od, lora=(z_t, z_u)),
+                              O.scaled_mm_ref(a, b, np.float32(0.5), None, od))
+    eye = np.zeros((64, 64), np.uint8)
+    eye[np.arange(64), np.arange(64)] = 0x3C
+    ones = np.ones((1, 64), np.float16)
+    s = np.float32(1 + 2.0**-11 - 2.0**-20)  # alone: just below the tie 1 + 2^-11 -> rounds to 1.0
+    t = np.full((1, 32), 2.0**-12)
+    u = np.full((64, 32), 2.0**-12)  # R * t * u = 2^-19 lifts it past the tie
+    y = O.scaled_mm_ref(ones, O.prepack_kn(eye), s, None, O.DT_F16, lora=(t, u))
+    assert np.all(y == np.float16(1 + 2.0**-10))
+    assert np.all(O.scaled_mm_ref(ones, O.prepack_kn(eye), s, None, O.DT_F16) == np.float16(1.0))
+
+
 def test_golden_fixtures_match_oracle():
     z = np.load(GOLDEN / "e5m2_codes.npz")
     assert np.array_equal(z["from_fp16"], O.e5m2_encode(ALL16.view(np.float16).astype(np.float32)))
