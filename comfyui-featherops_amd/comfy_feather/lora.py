@@ -8,8 +8,8 @@ Two forms:
   * apply_lora_patches(x, y, weight_functions): the reference's separate pass,
     y += F.linear(F.linear(x, down), up) * s per patch;
   * lora_factors(x, weight_functions): the factors of the same term for the
-    GEMM's fused epilogue -- T = [F.linear(x, down_i) * s_i]_i (M, R) and
-    U = [up_i]_i (N, R), concatenated over the patches along the rank and
+    GEMM's fused epilogue -- T = F.linear(x, [down_i * s_i]_i) (M, R) and
+    U = [up_i]_i (N, R), stacked over the patches along the rank and
     zero-padded to a multiple of 32, in x's dtype. The GEMM then adds T . U^T
     to its fp32 accumulator before rounding, so C is written once.
 """
@@ -48,23 +48,25 @@ def apply_lora_patches(x, y, weight_functions):
 
 def lora_factors(x: torch.Tensor, weight_functions):
     """(T, U) for the fused epilogue, or None when there is no patch or x is not
-    fp16/bf16 (then the separate pass keeps the reference's fp32 arithmetic)."""
+    fp16/bf16 (then the separate pass keeps the reference's fp32 arithmetic).
+
+    T comes from one F.linear of x with every patch's down matrix, scaled by its
+    strength and stacked along the rank, zero rows padding the rank to a
+    multiple of 32; U stacks the up matrices to match (zero columns)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         return None
     patches = _basic_patches(weight_functions)
     if not patches:
         return None
-    ts, us = [], []
+    downs, ups = [], []
     for down, up, scale in patches:
-        down = down.to(device=x.device, dtype=x.dtype)
-        up = up.to(device=x.device, dtype=x.dtype)
-        ts.append((F.linear(x, down).float() * scale).to(x.dtype))
-        us.append(up)
-    rank = sum(t.shape[1] for t in ts)
+        downs.append((down.to(device=x.device, dtype=torch.float32) * scale).to(x.dtype))
+        ups.append(up.to(device=x.device, dtype=x.dtype))
+    rank = sum(d.shape[0] for d in downs)
     pad = (-rank) % 32
     if pad:
-        ts.append(x.new_zeros(x.shape[0], pad))
-        us.append(x.new_zeros(us[0].shape[0], pad))
-    t = torch.cat(ts, dim=1) if len(ts) > 1 else ts[0].contiguous()
-    u = torch.cat(us, dim=1) if len(us) > 1 else us[0].contiguous()
-    return t, u
+        downs.append(x.new_zeros(pad, downs[0].shape[1]))
+        ups.append(x.new_zeros(ups[0].shape[0], pad))
+    t = F.linear(x, torch.cat(downs, dim=0) if len(downs) > 1 else downs[0])
+    u = torch.cat(ups, dim=1) if len(ups) > 1 else ups[0].contiguous()
+    return t.contiguous(), u
