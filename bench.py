@@ -235,6 +235,16 @@ def bench_configs(dev, op, quant, g):
     ev1.record()
     ev1.synchronize()
     q_ms = ev0.elapsed_time(ev1)
+    # the eager region above runs at the host's dispatch rate on boxes whose
+    # CPU is slower than ~50 us of device work per weight; the same 240 calls
+    # captured in a HIP graph and replayed give the device time alone
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qts_graph = [quant.make_feather_quantized_weight(w, None, torch.float16) for _, _, w, _ in raw]
+    graph.replay()
+    torch.cuda.synchronize()
+    q_dev_ms = time_launches(lambda _i: graph.replay(), 3)
+    del graph, qts_graph
     weights = []
     for (K, N, w, b5), qt in zip(raw, qts):
         bp5, s5 = quant.get_feather_plain_tensors(qt)
@@ -252,14 +262,56 @@ def bench_configs(dev, op, quant, g):
     elems = 40 * (4 * H * H + 2 * H * F)
     out["c5"] = {"blocks": 40, "linears": 240, "M": M5, "quantize_ms_total": round(q_ms, 2),
                  "quantize_GB_per_s": round(elems * 5 / (q_ms * 1e-3) / 1e9, 1),
+                 "quantize_device_ms_total": round(q_dev_ms, 2),
+                 "quantize_device_GB_per_s": round(elems * 5 / (q_dev_ms * 1e-3) / 1e9, 1),
+                 "quantize_timing": "eager: 240 calls between two events (host dispatch included); "
+                                    "device: the same calls replayed from a HIP graph",
                  "gemm_ms_total": round(gemm_ms, 2), "gemm_TFLOP_per_s": round(flop5 / (gemm_ms * 1e-3) / 1e12, 1),
                  "gemm_frac_fp16_peak": round(flop5 / (gemm_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
                  "end_to_end_ms": round(q_ms + gemm_ms, 2),
                  "weights_GB_e5m2": round(elems / 1e9, 2)}
-    log(f"bench: C5 quantize {q_ms:.1f} ms, GEMMs {gemm_ms:.1f} ms ({out['c5']['gemm_TFLOP_per_s']} TFLOP/s)")
+    log(f"bench: C5 quantize {q_ms:.1f} ms eager, {q_dev_ms:.1f} ms device, GEMMs {gemm_ms:.1f} ms "
+        f"({out['c5']['gemm_TFLOP_per_s']} TFLOP/s)")
     del weights, xs, outs
     torch.cuda.empty_cache()
     return out
+
+
+def bench_lora(dev, hk, g) -> dict:
+    """Unmerged LoRA (comfy_feather/lora.py) on the headline shape, bf16
+    activations and output, one rank-64 basic patch: the whole layer with the
+    term fused into the GEMM epilogue (T build + fused GEMM) against the
+    reference's separate pass (GEMM, then y += F.linear(F.linear(x, A), B) * s)."""
+    import importlib
+    from types import SimpleNamespace
+
+    import torch
+
+    lora = importlib.import_module("featherops_amd.comfy_feather.lora")
+    M, N, K, R = 32768, 13824, 5120, 64
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    bp = hk.prepack_b_for_scaled_mm((torch.randn(K, N, generator=g, device=dev) * 0.02).to(torch.float8_e5m2))
+    s = torch.tensor(1.0, device=dev)
+    bias = torch.zeros(N, dtype=torch.bfloat16, device=dev)
+    down = (torch.randn(R, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    up = (torch.randn(N, R, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wf = [SimpleNamespace(patches={"w": [(1.0, SimpleNamespace(weights=(up, down, float(R), None)), 1.0)]}, key="w")]
+
+    def fused(_i):
+        t, u = lora.lora_factors(x, wf)
+        return hk.scaled_mm_hip_any_m_lora(x, bp, s, bias, torch.bfloat16, t, u)
+
+    def separate(_i):
+        y = hk.scaled_mm_hip_any_m(x, bp, s, bias, torch.bfloat16)
+        return lora.apply_lora_patches(x, y, wf)
+
+    fused(0)
+    separate(0)
+    ms_f = time_launches(fused, 5)
+    ms_s = time_launches(separate, 5)
+    log(f"bench: LoRA rank {R} layer fused {ms_f:.3f} ms, separate {ms_s:.3f} ms")
+    return {"M": M, "N": N, "K": K, "rank": R, "dtype": "bf16", "fused_layer_ms": round(ms_f, 4),
+            "separate_layer_ms": round(ms_s, 4), "speedup": round(ms_s / ms_f, 3)}
 
 
 def main() -> int:
@@ -396,6 +448,7 @@ def main() -> int:
         log(f"bench: quantize {msq:.3f} ms per 13824x5120 weight")
 
     if not args.only_headline:
+        result["lora"] = bench_lora(dev, hk, g)
         result["configs"] = bench_configs(dev, op, quant, g)
 
     if not args.no_cpu:
