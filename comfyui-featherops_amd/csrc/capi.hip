@@ -191,6 +191,8 @@ bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, co
     if (lora_dtype != FEATHER_DTYPE_F16 && lora_dtype != FEATHER_DTYPE_BF16) return false;
     if (lora_t == nullptr || lora_u == nullptr || rank <= 0 || rank % 32 != 0 || rank > INT32_MAX / 2) return false;
     if ((reinterpret_cast<uintptr_t>(lora_t) | reinterpret_cast<uintptr_t>(lora_u)) % 16 != 0) return false;
+    // the factor copies address T and U with 32-bit lane offsets
+    if (M * rank * 2 > INT32_MAX || N * rank * 2 > INT32_MAX) return false;
     if (M == 0) return true;
     feather::MmArgs p;
     p.a = static_cast<const uint16_t*>(a);

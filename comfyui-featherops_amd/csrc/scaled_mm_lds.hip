@@ -33,10 +33,11 @@
 //     (their results are computed and dropped), so every copy is in bounds;
 //   * optional rank-R update in the epilogue (kLora, the unmerged LoRA side
 //     path of the reference's comfy_feather/lora.py:4-35): after the weight
-//     scale, acc += T(M x R) . U(N x R)^T on the fp16 or bf16 MFMA, from
-//     fragments read straight from global memory (both factors are small and
-//     shared by many tiles), before the rounding to the output type. The
-//     separate pass that would re-read and re-write C disappears.
+//     scale, acc += T(M x R) . U(N x R)^T on the fp16 or bf16 MFMA, before
+//     the rounding to the output type; the tile's rows of T and U go through
+//     the free stage buffers 64 ranks at a time (LDS-DMA, one round trip per
+//     64 ranks). The separate pass that would re-read and re-write C
+//     disappears.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -389,6 +390,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         // add the rank-R term in fp32 (one MFMA K step per 32 ranks; weights'
         // role for U, activations' role for T, so the accumulator layout is
         // the main loop's)
+        static_assert(kStage >= BM * 128 && kStage >= BN * 128, "a 64-rank chunk of T or U must fit a stage buffer");
 #pragma unroll
         for (int rm = 0; rm < RM; ++rm)
 #pragma unroll
@@ -396,29 +398,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[rm][rn][i] = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
-        const int trow0 = m0 + wave_m * WTM + lr;
-        const int ucol0 = n0 + wave_n * WTN + lr;
-        for (int r0 = 0; r0 < lora_rank; r0 += 32) {
-            uint4 tf[RM], uf[RN];
-#pragma unroll
-            for (int rm = 0; rm < RM; ++rm) {
-                const int row = trow0 + rm * 16 < M ? trow0 + rm * 16 : M - 1;
-                tf[rm] = *reinterpret_cast<const uint4*>(lora_t + static_cast<int64_t>(row) * lora_rank + r0 + 8 * lg);
+        // 64 ranks at a time, the tile's T rows and U rows are copied into the
+        // (now free) stage buffers with the A operand's layout (128-byte rows,
+        // chunk c at c ^ swz(row)), one round trip for the whole tile, and the
+        // MFMA steps read their fragments from LDS. Step kh covers ranks
+        // [32 kh, 32 kh + 32): lane group lg reads chunk lg + 4 kh of T and U.
+        // A 32-rank tail copies ranks [0, 32) only and runs step 0.
+        const uint32_t lt = lds_addr_of(sbuf0);
+        const uint32_t lu = lds_addr_of(sbuf1);
+        constexpr int kTInst = BM / 8;  // 1 KB copies: 8 rows of 64 ranks
+        constexpr int kUInst = BN / 8;
+        for (int r0 = 0; r0 < lora_rank; r0 += 64) {
+            const bool tail = lora_rank - r0 < 64;
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the buffers are done
+            stage_barrier();                      // and every other wave's
+            for (int j = wave; j < kTInst + kUInst; j += kWaves) {
+                const bool is_t = j < kTInst;
+                const int jj = is_t ? j : j - kTInst;
+                const int row = jj * 8 + (lane >> 3);
+                int c = (lane & 7) ^ swz(row);
+                if (tail && c >= 4) c -= 4;  // past the rank: a valid chunk, never read
+                const int grow = is_t ? (m0 + row < M ? m0 + row : M - 1) : (n0 + row < N ? n0 + row : N - 1);
+                dma16_lds(is_t ? lora_t : lora_u, static_cast<uint32_t>((grow * lora_rank + r0 + 8 * c) * 2),
+                          (is_t ? lt : lu) + jj * 1024);
             }
+            wait_vmcnt<0>();
+            stage_barrier();
+            for (int kh = 0; kh < (tail ? 1 : 2); ++kh) {
+                uint4 tf[RM], uf[RN];
 #pragma unroll
-            for (int rn = 0; rn < RN; ++rn) {
-                const int col = ucol0 + rn * 16 < N ? ucol0 + rn * 16 : N - 1;
-                uf[rn] = *reinterpret_cast<const uint4*>(lora_u + static_cast<int64_t>(col) * lora_rank + r0 + 8 * lg);
-            }
-#pragma unroll
-            for (int rm = 0; rm < RM; ++rm)
+                for (int rm = 0; rm < RM; ++rm) {
+                    const int row = wave_m * WTM + rm * 16 + lr;
+                    tf[rm] = lds_ld16(lt + row * 128 + (((lg + 4 * kh) ^ swz(row)) << 4));
+                }
 #pragma unroll
                 for (int rn = 0; rn < RN; ++rn) {
-                    if constexpr (kLora == 1)
-                        acc[rm][rn] = mfma16x16x32(as_half8(uf[rn]), as_half8(tf[rm]), acc[rm][rn]);
-                    else
-                        acc[rm][rn] = mfma16x16x32_bf16(uf[rn], tf[rm], acc[rm][rn]);
+                    const int row = wave_n * WTN + rn * 16 + lr;
+                    uf[rn] = lds_ld16(lu + row * 128 + (((lg + 4 * kh) ^ swz(row)) << 4));
                 }
+#pragma unroll
+                for (int rm = 0; rm < RM; ++rm)
+#pragma unroll
+                    for (int rn = 0; rn < RN; ++rn) {
+                        if constexpr (kLora == 1)
+                            acc[rm][rn] = mfma16x16x32(as_half8(uf[rn]), as_half8(tf[rm]), acc[rm][rn]);
+                        else
+                            acc[rm][rn] = mfma16x16x32_bf16(uf[rn], tf[rm], acc[rm][rn]);
+                    }
+            }
         }
     }
 

@@ -112,8 +112,9 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
  * comfy_feather/lora.py:4-35 for the part after F.linear(x, A): the caller
  * computes T = F.linear(x, A) * s. Served by the LDS-DMA tiles (K % 64 == 0,
  * a routed tile of at least 128 x 128) with fp16 activations and e5m2
- * weights; returns false and launches nothing otherwise (the caller then
- * adds the term itself). Needs no workspace.
+ * weights, with M * rank and N * rank below 2^30; returns false and
+ * launches nothing otherwise (the caller then adds the term itself). Needs no
+ * workspace.
  */
 bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
                                    uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
