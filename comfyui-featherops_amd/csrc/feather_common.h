@@ -83,12 +83,11 @@ __device__ __forceinline__ float out_bits_to_f32(uint16_t b) {
     else return half_bits_to_f32(b);
 }
 
-// Widen 8 fp8 bytes (two dwords, byte j = element j) into 8 fp16 lanes.
+// Widen 8 fp8 bytes (two dwords, byte j = element j) into 8 fp16 lanes,
+// exactly (every fp8 value of either format is an fp16 value).
 // e5m2: element j -> (byte_j << 8); one v_perm_b32 per output dword.
-// e4m3fn: element j -> ((byte_j & 0x7f) << 7) | ((byte_j & 0x80) << 8), i.e.
-// the code re-read with fp16's bias, which is the true value * 2^-8 for every
-// finite code (subnormals included); the caller multiplies the fp32 result by
-// 256. The two NaN codes decode to the finite +-1.875*2^-8.
+// e4m3fn: gfx950's OCP fp8 -> f16 conversion with scale 1 (two elements per
+// instruction; subnormals exact, the two NaN codes -> NaN).
 template <bool kE4m3>
 __device__ __forceinline__ half8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
     uint32_t w0, w1, w2, w3;
@@ -99,14 +98,10 @@ __device__ __forceinline__ half8_t widen_fp8x8(uint32_t lo, uint32_t hi) {
         w2 = __builtin_amdgcn_perm(0u, hi, 0x010c000cu);
         w3 = __builtin_amdgcn_perm(0u, hi, 0x030c020cu);
     } else {
-        const uint32_t p0 = __builtin_amdgcn_perm(0u, lo, 0x0c010c00u);
-        const uint32_t p1 = __builtin_amdgcn_perm(0u, lo, 0x0c030c02u);
-        const uint32_t p2 = __builtin_amdgcn_perm(0u, hi, 0x0c010c00u);
-        const uint32_t p3 = __builtin_amdgcn_perm(0u, hi, 0x0c030c02u);
-        w0 = ((p0 & 0x007f007fu) << 7) | ((p0 & 0x00800080u) << 8);
-        w1 = ((p1 & 0x007f007fu) << 7) | ((p1 & 0x00800080u) << 8);
-        w2 = ((p2 & 0x007f007fu) << 7) | ((p2 & 0x00800080u) << 8);
-        w3 = ((p3 & 0x007f007fu) << 7) | ((p3 & 0x00800080u) << 8);
+        w0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
+        w1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
+        w2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
+        w3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
     }
     uint4 v = make_uint4(w0, w1, w2, w3);
     return __builtin_bit_cast(half8_t, v);

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             for (int rn = 0; rn < RN; ++rn)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[rm][rn][i] = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
+                    acc[rm][rn][i] = opaque_f32(acc[rm][rn][i] * s);
         // 64 ranks at a time, the tile's T rows and U rows are copied into the
         // (now free) stage buffers with the A operand's layout (128-byte rows,
         // chunk c at c ^ swz(row)), one round trip for the whole tile, and the
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 v[i] = kLora != 0 ? acc[rm][rn][i]
-                                  : opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
+                                  : opaque_f32(acc[rm][rn][i] * s);
             // row lr, columns 4*lg .. 4*lg+3 of this 16x16 tile: one 8-byte write
             const int chunk = (2 * rn + (lg >> 1) + row) % kCPR;
             *reinterpret_cast<uint2*>(sc + row * kRowBytes + chunk * 16 + (lg & 1) * 8) =

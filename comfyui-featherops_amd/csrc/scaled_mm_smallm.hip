@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) sum += red[w][r][c];
         }
-        const float v = opaque_f32(kE4m3 ? (sum * 256.0f) * s : sum * s);
+        const float v = opaque_f32(sum * s);
         uint16_t o = f32_to_out_bits<kBf16>(v);
         if (has_bias) o = f32_to_out_bits<kBf16>(out_bits_to_f32<kBf16>(o) + out_bits_to_f32<kBf16>(bias[n0 + c]));
         C[static_cast<int64_t>(r) * N + n0 + c] = o;

@@ -203,8 +203,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_tile_kernel(
         for (int rn = 0; rn < RN; ++rn) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                // e4m3 codes were widened as value * 2^-8; * 256 restores them exactly
-                const float v = opaque_f32(kE4m3 ? (acc[rm][rn][i] * 256.0f) * s : acc[rm][rn][i] * s);
+                const float v = opaque_f32(acc[rm][rn][i] * s);
                 *reinterpret_cast<uint16_t*>(sc + (4 * lg + i) * kCRowBytes + (rn * 16 + lr) * 2) =
                     f32_to_out_bits<kBf16>(v);
             }

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from conftest import GOLDEN
-from gpu_util import assert_gemm_close, capi_scaled_mm, to_dev_codes, weight_like
+from gpu_util import assert_gemm_close, capi_scaled_mm, lib, stream, to_dev_codes, weight_like
 from oracle import feather_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -370,3 +370,51 @@ def test_size_one_dims_any_stride(cuda, hk):
     # the op's validation also accepts an M = 1 output with any row stride
     c = torch.empty((1, N), dtype=torch.float16, device=cuda).as_strided((1, N), (5, 1))
     hk.validate_scaled_mm(ad, bd, torch.tensor(s, device=cuda), None, c, 1, 1, 1, 1, 2, 1, block_divisible=False)
+
+
+@pytest.mark.parametrize("b_dtype", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("route", ["small_m", "tile", "lds", "split_k"])
+def test_every_fp8_code_decodes_exactly(cuda, b_dtype, route):
+    """All 256 weight codes through each kernel family: column n of B holds
+    code n in its first K row and zeros below, A's rows are e_0, so C[:, n]
+    is exactly the decoded code (NaN codes NaN, e5m2 infinities inf; -0
+    comes out as +0 because the accumulator starts at +0)."""
+    import os
+
+    M, K, splitk = {"small_m": (16, 16, None), "tile": (256, 16, "0"), "lds": (256, 64, "0"),
+                    "split_k": (256, 64, "1")}[route]
+    cfg = (1, 1, 2, 1, 2) if route == "small_m" else (2, 4, 4, 8, 4) if route == "lds" else (2, 2, 2, 4, 4)
+    N = 256
+    codes = torch.zeros(K, N, dtype=torch.uint8)
+    codes[0] = torch.arange(256, dtype=torch.uint8)
+    bp = codes.view(K // 16, 16, N).permute(0, 2, 1).contiguous().to(cuda)
+    a = torch.zeros(M, K, dtype=torch.float16)
+    a[:, 0] = 1.0
+    a = a.to(cuda)
+    c = torch.full((M, N), 7.0, dtype=torch.float16, device=cuda)
+    L = lib()
+    b_code = 0 if b_dtype == torch.float8_e4m3fn else 1
+    old = os.environ.get("FEATHEROPS_SPLITK")
+    try:
+        if splitk is not None:
+            os.environ["FEATHEROPS_SPLITK"] = splitk
+        kid = L.feather_scaled_mm_kernel_id(M, N, K, *cfg)
+        want_kid = {"small_m": (10, 10), "tile": (1, 9), "lds": (20, 29), "split_k": (30, 39)}[route]
+        assert want_kid[0] <= kid <= want_kid[1], f"{route}: kernel id {kid}"
+        ws_bytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
+        ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=cuda)
+        ok = L.feather_launch_scaled_mm_ws(a.data_ptr(), bp.data_ptr(), None, None, c.data_ptr(), M, N, K, 0, 0, *cfg,
+                                           b_code, 0, ws.data_ptr(), ws.numel(), stream(cuda))
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            os.environ.pop("FEATHEROPS_SPLITK", None)
+        else:
+            os.environ["FEATHEROPS_SPLITK"] = old
+    assert ok
+    dec = O.e4m3fn_decode(np.arange(256)) if b_code == 0 else O.e5m2_decode(np.arange(256, dtype=np.uint8))
+    want = torch.from_numpy(dec.astype(np.float32)).to(torch.float16).expand(M, N)
+    got = c.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(want)), route
+    fin = ~torch.isnan(want)
+    assert torch.equal(got[fin], want[fin]), route
