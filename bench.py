@@ -229,15 +229,24 @@ def bench_configs(dev, op, quant, g):
     qts = [quant.make_feather_quantized_weight(w, None, torch.float16) for _, _, w, _ in raw]
     del qts
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    qts = [quant.make_feather_quantized_weight(w, None, torch.float16) for _, _, w, _ in raw]
-    ev1.record()
-    ev1.synchronize()
-    q_ms = ev0.elapsed_time(ev1)
-    # the eager region above runs at the host's dispatch rate on boxes whose
-    # CPU is slower than ~50 us of device work per weight; the same 240 calls
-    # captured in a HIP graph and replayed give the device time alone
+    # three eager passes: torch's caching allocator now and then frees and
+    # re-maps device memory inside such a pass (a pass then takes ~4x longer
+    # with the host blocked in the allocator); the best pass is reported with
+    # all three
+    q_passes = []
+    for rep in range(3):
+        if rep:
+            del qts
+            torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        qts = [quant.make_feather_quantized_weight(w, None, torch.float16) for _, _, w, _ in raw]
+        ev1.record()
+        ev1.synchronize()
+        q_passes.append(ev0.elapsed_time(ev1))
+    q_ms = min(q_passes)
+    # the same 240 calls captured in a HIP graph and replayed: the device time
+    # alone (no launch gaps, no allocator)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         qts_graph = [quant.make_feather_quantized_weight(w, None, torch.float16) for _, _, w, _ in raw]
@@ -264,8 +273,9 @@ def bench_configs(dev, op, quant, g):
                  "quantize_GB_per_s": round(elems * 5 / (q_ms * 1e-3) / 1e9, 1),
                  "quantize_device_ms_total": round(q_dev_ms, 2),
                  "quantize_device_GB_per_s": round(elems * 5 / (q_dev_ms * 1e-3) / 1e9, 1),
-                 "quantize_timing": "eager: 240 calls between two events (host dispatch included); "
-                                    "device: the same calls replayed from a HIP graph",
+                 "quantize_eager_passes_ms": [round(x, 2) for x in q_passes],
+                 "quantize_timing": "eager: 240 calls between two events (host dispatch included), best of three "
+                                    "passes; device: the same calls replayed from a HIP graph",
                  "gemm_ms_total": round(gemm_ms, 2), "gemm_TFLOP_per_s": round(flop5 / (gemm_ms * 1e-3) / 1e12, 1),
                  "gemm_frac_fp16_peak": round(flop5 / (gemm_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
                  "end_to_end_ms": round(q_ms + gemm_ms, 2),

@@ -29,6 +29,9 @@ import torch
 
 from ..kernel.hip import _lib
 
+# the quantize ops (torch.ops.feather_ops.quantize_prepack_e5m2[_scaled]) live in the C++ op library
+_lib.load_torch_ops()
+
 try:  # ComfyUI host process
     import comfy.float as _comfy_float
     from comfy.quant_ops import QuantizedLayout, QuantizedTensor, register_layout_class
@@ -161,29 +164,12 @@ def _dtype_code(dtype: torch.dtype) -> int:
 
 def _quantize_2d(w2d: torch.Tensor, native: bool, ckpt_scale: torch.Tensor | None,
                  given_scale: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
-    """(N, K) GPU tensor -> ((K/16, N, 16) e5m2, fp32 scale) via the fused kernel."""
-    N, K = w2d.shape
-    dev = w2d.device
-    code = _dtype_code(w2d.dtype)
-    src = w2d.contiguous()
-    out = torch.empty((K // 16, N, 16), dtype=torch.float8_e5m2, device=dev)
-    L = _lib.lib()
-    with torch.cuda.device(dev):
-        stream = _lib.stream_ptr(dev)
-        if given_scale is not None:
-            s = given_scale.reshape(1).to(device=dev, dtype=torch.float32).contiguous()
-            _lib.check(L.feather_quantize_prepack_e5m2_scaled(src.data_ptr(), code, N, K, s.data_ptr(),
-                                                              out.data_ptr(), stream), "quantize_prepack")
-            return out, given_scale
-        scale_out = torch.empty((), dtype=torch.float32, device=dev)
-        workspace = torch.empty(256, dtype=torch.int32, device=dev)  # partial maxima (1 KB)
-        cs = None
-        if ckpt_scale is not None:
-            cs = ckpt_scale.reshape(1).to(device=dev, dtype=torch.float32).contiguous()
-        _lib.check(L.feather_quantize_prepack_e5m2(src.data_ptr(), code, N, K, cs.data_ptr() if cs is not None else None,
-                                                   1 if native else 0, out.data_ptr(), scale_out.data_ptr(),
-                                                   workspace.data_ptr(), stream), "quantize_prepack")
-    return out, scale_out
+    """(N, K) GPU tensor -> ((K/16, N, 16) e5m2, fp32 scale) via the fused kernel
+    (torch.ops.feather_ops.quantize_prepack_e5m2[_scaled], registered in C++)."""
+    _dtype_code(w2d.dtype)
+    if given_scale is not None:
+        return torch.ops.feather_ops.quantize_prepack_e5m2_scaled.default(w2d, given_scale), given_scale
+    return torch.ops.feather_ops.quantize_prepack_e5m2.default(w2d, ckpt_scale, native)
 
 
 def _scale_arg(scale, device) -> torch.Tensor | None:
@@ -293,15 +279,10 @@ def make_feather_quantized_weight(weight, scale, orig_dtype):
     weight is quantized from float32(weight) * scale (fused in the kernel)."""
     if weight.ndim != 2:
         raise ValueError(f"Feather FP8 packed weights require a 2D tensor, got {weight.ndim}D")
-    if scale is None:
-        scale_t = torch.ones((), device=weight.device, dtype=torch.float32)
-        ckpt = None
-    else:
-        scale_t = scale.to(device=weight.device, dtype=torch.float32)
-        ckpt = scale_t
+    ckpt = None if scale is None else scale.to(device=weight.device, dtype=torch.float32)
     if weight.dtype == torch.float8_e5m2:
         qdata = prepack_transpose(weight)
-        out_scale = scale_t
+        out_scale = ckpt if ckpt is not None else torch.ones((), device=weight.device, dtype=torch.float32)
     else:
         if weight.shape[1] % 16 != 0:
             raise RuntimeError(f"K ({weight.shape[1]}) must be divisible by 16")

@@ -8,6 +8,8 @@
 //   feather_ops::scaled_mm_any_m_lora
 //                                 the any-M op plus an unmerged-LoRA term,
 //                                 fused into the epilogue on the large tiles
+//   feather_ops::quantize_prepack_e5m2(_scaled)
+//                                 the fused quantize + prepack of a weight
 //   feather_ops_internal::scaled_mm_configured
 //                                 the reference's configured op (hip_kernel.py:
 //                                 12-58, a Python custom op there), Meta kernel
@@ -289,6 +291,69 @@ at::Tensor scaled_mm_any_m_lora_meta(const at::Tensor& a, const at::Tensor& b_pr
     return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
 }
 
+int weight_dtype_code(const at::Tensor& w) {
+    switch (w.scalar_type()) {
+        case at::kHalf: return FEATHER_DTYPE_F16;
+        case at::kBFloat16: return FEATHER_DTYPE_BF16;
+        case at::kFloat: return FEATHER_DTYPE_F32;
+        default:
+            TORCH_CHECK(false, "FeatherOps quantization supports float16, bfloat16 and float32 inputs, got ",
+                        w.scalar_type());
+    }
+    return -1;
+}
+
+void check_weight(const at::Tensor& w) {
+    TORCH_CHECK(w.is_cuda(), "w must be a CUDA tensor");
+    TORCH_CHECK(w.dim() == 2, "w must be 2D (N, K)");
+    TORCH_CHECK(w.size(1) % 16 == 0, "K (", w.size(1), ") must be divisible by 16");
+}
+
+// feather_ops::quantize_prepack_e5m2 (reference comfy_feather/quant.py:52-74 +
+// prepack_transpose, quant.py:11-13): (N, K) fp16/bf16/fp32 weight -> the
+// (K/16, N, 16) e5m2 codes and the fp32 per-tensor scale. native = false is
+// the load path (fp32 arithmetic on w * ckpt_scale), native = true the patch
+// path (arithmetic in w's dtype, fp16 reciprocal clamp).
+std::tuple<at::Tensor, at::Tensor> quantize_prepack_e5m2(const at::Tensor& w, const std::optional<at::Tensor>& ckpt_scale,
+                                                         bool native) {
+    check_weight(w);
+    const int code = weight_dtype_code(w);
+    const at::Tensor src = w.contiguous();
+    const int64_t N = src.size(0), K = src.size(1);
+    const c10::DeviceGuard guard(src.device());
+    at::Tensor out = at::empty({K / 16, N, 16}, src.options().dtype(at::kFloat8_e5m2));
+    at::Tensor scale = at::empty({}, src.options().dtype(at::kFloat));
+    at::Tensor workspace = at::empty({256}, src.options().dtype(at::kInt));  // partial maxima (1 KB)
+    at::Tensor cs;
+    if (ckpt_scale.has_value()) cs = ckpt_scale->reshape({1}).to(src.device(), at::kFloat).contiguous();
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(src.device().index()).stream();
+    const int st = feather_quantize_prepack_e5m2(src.data_ptr(), code, N, K,
+                                                 cs.defined() ? static_cast<const float*>(cs.data_ptr()) : nullptr,
+                                                 native ? 1 : 0, static_cast<uint8_t*>(out.data_ptr()),
+                                                 static_cast<float*>(scale.data_ptr()),
+                                                 static_cast<uint32_t*>(workspace.data_ptr()), stream);
+    TORCH_CHECK(st == FEATHER_OK, "quantize_prepack failed: ", feather_status_string(st), " (status ", st, ")");
+    return {out, scale};
+}
+
+// feather_ops::quantize_prepack_e5m2_scaled: the same with a given scale
+// (quant.py:59-74 when `scale` is passed; no amax, no clamp).
+at::Tensor quantize_prepack_e5m2_scaled(const at::Tensor& w, const at::Tensor& scale) {
+    check_weight(w);
+    const int code = weight_dtype_code(w);
+    const at::Tensor src = w.contiguous();
+    const int64_t N = src.size(0), K = src.size(1);
+    const c10::DeviceGuard guard(src.device());
+    at::Tensor out = at::empty({K / 16, N, 16}, src.options().dtype(at::kFloat8_e5m2));
+    const at::Tensor s = scale.reshape({1}).to(src.device(), at::kFloat).contiguous();
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(src.device().index()).stream();
+    const int st = feather_quantize_prepack_e5m2_scaled(src.data_ptr(), code, N, K,
+                                                        static_cast<const float*>(s.data_ptr()),
+                                                        static_cast<uint8_t*>(out.data_ptr()), stream);
+    TORCH_CHECK(st == FEATHER_OK, "quantize_prepack failed: ", feather_status_string(st), " (status ", st, ")");
+    return out;
+}
+
 at::Tensor scaled_mm_any_m_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
                                 const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
                                 at::ScalarType out_dtype) {
@@ -303,12 +368,16 @@ TORCH_LIBRARY(feather_ops, m) {
     m.def("scaled_mm_any_m(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype) -> Tensor");
     m.def("scaled_mm_any_m_lora(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, ScalarType out_dtype, "
           "Tensor lora_t, Tensor lora_u) -> Tensor");
+    m.def("quantize_prepack_e5m2(Tensor w, Tensor? ckpt_scale, bool native) -> (Tensor, Tensor)");
+    m.def("quantize_prepack_e5m2_scaled(Tensor w, Tensor scale) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm", &scaled_mm);
     m.impl("scaled_mm_any_m", &scaled_mm_any_m);
     m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora);
+    m.impl("quantize_prepack_e5m2", &quantize_prepack_e5m2);
+    m.impl("quantize_prepack_e5m2_scaled", &quantize_prepack_e5m2_scaled);
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, Meta, m) {

@@ -173,6 +173,14 @@ def test_native_op_registered_in_cpp(hk):
         "-> Tensor")
     assert torch._C._dispatch_has_kernel_for_dispatch_key(cfg.name(), "Meta")
     assert hk.scaled_mm_hip_configured is cfg
+    q = torch.ops.feather_ops.quantize_prepack_e5m2.default
+    assert str(q._schema) == ("feather_ops::quantize_prepack_e5m2(Tensor w, Tensor? ckpt_scale, bool native) "
+                              "-> (Tensor, Tensor)")
+    qs = torch.ops.feather_ops.quantize_prepack_e5m2_scaled.default
+    assert str(qs._schema) == "feather_ops::quantize_prepack_e5m2_scaled(Tensor w, Tensor scale) -> Tensor"
+    for op_ in (q, qs):
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op_.name(), "CUDA")
+        assert "csrc/torch_op.cpp" in torch._C._dispatch_dump(op_.name())
 
 
 def test_op_library_loads_first_in_fresh_process():
