@@ -77,3 +77,41 @@ def test_random_configured(cuda, hk, seed):
                                         bias.to(cuda) if has_b else None, out, *cfg)
         torch.cuda.synchronize()
         assert_gemm_close(y, ref, out, f"seed {seed} case {case}: cfg={cfg} M={M} N={N} K={K} {out} e4m3={e4}")
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_any_m_lora(cuda, hk, seed):
+    """scaled_mm_hip_any_m_lora over random shapes (fused LDS-tile route and
+    the fallback routes), ranks, factor and output dtypes: the fused route
+    against the oracle's lora= contract (term added before the output
+    rounding), the others against the GEMM output plus the term rounded to the
+    output type."""
+    rng = np.random.default_rng(200 + seed)
+    for case in range(16):
+        M = int(rng.choice([17, 64, 300, 1024, 2048]))
+        N = int(rng.choice([256, 768, 2048, 3072]))
+        K = int(rng.choice([256, 512, 1040]))
+        R = 32 * int(rng.integers(1, 5))
+        out = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        fdt = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        g = torch.Generator().manual_seed(3000 * seed + case)
+        a = torch.randn(M, K, generator=g).half()
+        packed, s = weight_like(N, K, g)
+        bias = (torch.randn(N, generator=g) * 0.5).to(out)
+        t = (torch.randn(M, R, generator=g) * 0.2).to(fdt)
+        u = (torch.randn(N, R, generator=g) * 0.05).to(fdt)
+        y = hk.scaled_mm_hip_any_m_lora(a.to(cuda), to_dev_codes(packed, cuda), torch.tensor(s, device=cuda),
+                                        bias.to(cuda), out, t.to(cuda), u.to(cuda))
+        torch.cuda.synchronize()
+        od = O.DT_F16 if out == torch.float16 else O.DT_BF16
+        kid = hk.kernel_id(M, N, K, hk.any_m_config(M, N, K))
+        label = f"seed {seed} case {case}: M={M} N={N} K={K} R={R} {out} {fdt} kid={kid}"
+        if 20 <= kid < 30:
+            ref = O.scaled_mm_ref(a.numpy(), packed, s, _bias_np(bias, out), od,
+                                  lora=(t.double().numpy(), u.double().numpy()))
+        else:
+            base = O.scaled_mm_ref(a.numpy(), packed, s, _bias_np(bias, out), od)
+            base = torch.from_numpy(O.bf16_bits_to_f32(base) if base.dtype == np.uint16 else base.astype(np.float32))
+            yr = base.to(out) + torch.mm(t, u.t()).to(out)
+            ref = yr.numpy() if out == torch.float16 else yr.view(torch.int16).numpy().view(np.uint16)
+        assert_gemm_close(y, ref, out, label)
