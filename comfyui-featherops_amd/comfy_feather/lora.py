@@ -46,18 +46,9 @@ def apply_lora_patches(x, y, weight_functions):
     return y
 
 
-def lora_factors(x: torch.Tensor, weight_functions):
-    """(T, U) for the fused epilogue, or None when there is no patch or x is not
-    fp16/bf16 (then the separate pass keeps the reference's fp32 arithmetic).
-
-    T comes from one F.linear of x with every patch's down matrix, scaled by its
-    strength and stacked along the rank, zero rows padding the rank to a
-    multiple of 32; U stacks the up matrices to match (zero columns)."""
-    if x.dtype not in (torch.float16, torch.bfloat16):
-        return None
-    patches = _basic_patches(weight_functions)
-    if not patches:
-        return None
+def _stacked_factors(x: torch.Tensor, patches):
+    """[down_i * s_i]_i (R, K) and [up_i]_i (N, R) in x's dtype on x's device,
+    the rank zero-padded to a multiple of 32."""
     downs, ups = [], []
     for down, up, scale in patches:
         downs.append((down.to(device=x.device, dtype=torch.float32) * scale).to(x.dtype))
@@ -67,6 +58,38 @@ def lora_factors(x: torch.Tensor, weight_functions):
     if pad:
         downs.append(x.new_zeros(pad, downs[0].shape[1]))
         ups.append(x.new_zeros(ups[0].shape[0], pad))
-    t = F.linear(x, torch.cat(downs, dim=0) if len(downs) > 1 else downs[0])
+    d = torch.cat(downs, dim=0) if len(downs) > 1 else downs[0].contiguous()
     u = torch.cat(ups, dim=1) if len(ups) > 1 else ups[0].contiguous()
-    return t.contiguous(), u
+    return d, u
+
+
+def lora_factors(x: torch.Tensor, weight_functions, cache: dict | None = None):
+    """(T, U) for the fused epilogue, or None when there is no patch or x is not
+    fp16/bf16 (then the separate pass keeps the reference's fp32 arithmetic).
+
+    T comes from one F.linear of x with every patch's down matrix, scaled by its
+    strength and stacked along the rank, zero rows padding the rank to a
+    multiple of 32; U stacks the up matrices to match (zero columns).
+
+    `cache` (a dict the caller keeps, e.g. one per layer) holds the stacked
+    matrices between calls. An entry is reused only while the patch list holds
+    the same tensor objects, unmodified in place (version counters), with the
+    same strengths, and x has the same dtype and device; the entry keeps the
+    tensors themselves, so their ids cannot be recycled while it lives."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    patches = _basic_patches(weight_functions)
+    if not patches:
+        return None
+    if cache is None:
+        d, u = _stacked_factors(x, patches)
+    else:
+        key = (x.dtype, x.device, tuple((id(dn), dn._version, id(up), up._version, float(sc))
+                                        for dn, up, sc in patches))
+        hit = cache.get("entry")
+        if hit is not None and hit[0] == key:
+            d, u = hit[2], hit[3]
+        else:
+            d, u = _stacked_factors(x, patches)
+            cache["entry"] = (key, [(dn, up) for dn, up, _ in patches], d, u)
+    return F.linear(x, d).contiguous(), u

@@ -194,7 +194,11 @@ def feather_ops(out_dtype=torch.bfloat16, excluded_names=()):
                     y = apply_lora_patches(x, y, self.weight_function)
                 else:
                     # basic LoRA patches go into the GEMM's epilogue (one pass over C)
-                    lora = lora_factors(x, self.weight_function) if self.fuse_lora else None
+                    if self.fuse_lora:
+                        cache = self.__dict__.setdefault("_lora_factor_cache", {})
+                        lora = lora_factors(x, self.weight_function, cache)
+                    else:
+                        lora = None
                     y = self._forward_padded(x, lora)
                     if lora is None:
                         y = apply_lora_patches(x, y, self.weight_function)

@@ -74,3 +74,26 @@ def test_non_basic_patches_raise(lora, bad):
         lora.apply_lora_patches(x, torch.zeros(2, 8, dtype=torch.float16), [bad])
     with pytest.raises(NotImplementedError, match="basic LoRA"):
         lora.lora_factors(x, [bad])
+
+
+def test_factor_cache_reuse_and_invalidation(lora):
+    """The stacked factors are reused while the patches are the same, unmodified
+    tensors with the same strengths, and rebuilt when any of that changes."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(5, 64, generator=g).to(torch.bfloat16)
+    wf, _ = make_patches(40, 64, [8, 16], g, dtype=torch.bfloat16)
+    cache = {}
+    t0, u0 = lora.lora_factors(x, wf, cache)
+    entry = cache["entry"]
+    t1, u1 = lora.lora_factors(x, wf, cache)
+    assert cache["entry"] is entry and u1 is u0 and torch.equal(t1, t0)
+    assert torch.equal(t0, lora.lora_factors(x, wf)[0])  # same values as without a cache
+    patch = wf[0].patches["w"][0]
+    patch[1].weights[0].mul_(2.0)  # up of the first patch changed in place
+    _, u2 = lora.lora_factors(x, wf, cache)
+    assert cache["entry"] is not entry and torch.equal(u2[:, :8], u0[:, :8] * 2)
+    entry = cache["entry"]
+    wf[0].patches["w"][0] = (0.5,) + patch[1:]  # new strength
+    t3, _ = lora.lora_factors(x, wf, cache)
+    assert cache["entry"] is not entry
+    assert torch.equal(t3, lora.lora_factors(x, wf)[0])
