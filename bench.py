@@ -334,7 +334,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported on this single-GPU build "
-              "(see the sharding notes in DESIGN.md)", file=sys.stderr)
+              "(the kernel runs on one GPU's shard; multi-GPU sharding is design-only here)", file=sys.stderr)
         return 2
 
     import numpy as np
