@@ -23,7 +23,7 @@ untouched (the fused kernel never materialises the scaled copy).
 
 from __future__ import annotations
 
-from dataclasses import dataclass, fields
+from dataclasses import dataclass, replace
 
 import torch
 
@@ -131,28 +131,23 @@ class FeatherFP8E5M2PackedParams:
     orig_dtype: torch.dtype
     orig_shape: tuple[int, ...]
 
+    # the one tensor-valued field; the rest is plain metadata
+    _TENSORS = ("scale",)
+
     def _tensor_fields(self):
-        return ["scale"]
+        return list(self._TENSORS)
 
     def to_device(self, device):
-        kwargs = {f.name: getattr(self, f.name) for f in fields(self)}
-        for field in self._tensor_fields():
-            kwargs[field] = kwargs[field].to(device=device)
-        return type(self)(**kwargs)
+        return replace(self, scale=self.scale.to(device=device))
 
     def clone(self):
-        kwargs = {f.name: getattr(self, f.name) for f in fields(self)}
-        for field in self._tensor_fields():
-            kwargs[field] = kwargs[field].clone()
-        return type(self)(**kwargs)
+        return replace(self, scale=self.scale.clone())
 
     def copy_from(self, src, non_blocking=False):
-        for field in fields(self):
-            src_value = getattr(src, field.name)
-            if field.name in self._tensor_fields():
-                getattr(self, field.name).copy_(src_value, non_blocking=non_blocking)
-            else:
-                object.__setattr__(self, field.name, src_value)
+        """In-place update: the scale tensor keeps its storage, the metadata is taken from src."""
+        self.scale.copy_(src.scale, non_blocking=non_blocking)
+        for name in ("orig_dtype", "orig_shape"):
+            object.__setattr__(self, name, getattr(src, name))
 
 
 def _dtype_code(dtype: torch.dtype) -> int:

@@ -54,9 +54,15 @@ int tile_kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     return feather::kTile64x64;
 }
 
+// Shape limits every kernel family relies on: the LDS kernels build per-lane copy offsets
+// within a tile as 32-bit products (row * K * 2 over 256 rows, (3 * N + column) * 16 over a
+// 4-group stage), so K < 2^22 and N < 2^25 keep them below 2^31; M and (K/16) * N stay 32-bit.
+constexpr int64_t kMaxK = int64_t{1} << 22;
+constexpr int64_t kMaxN = int64_t{1} << 25;
+
 bool sizes_ok(int64_t M, int64_t N, int64_t K) {
     const int64_t lim = INT32_MAX;
-    return M >= 0 && N > 0 && K > 0 && M <= lim && N <= lim && K <= lim && N % 16 == 0 && K % 16 == 0 &&
+    return M >= 0 && N > 0 && K > 0 && M <= lim && N < kMaxN && K < kMaxK && N % 16 == 0 && K % 16 == 0 &&
            (K / 16) * N <= lim;
 }
 

@@ -90,3 +90,74 @@ def weight_like(N, K, gen, std=0.02):
 
 def to_dev_codes(packed: np.ndarray, dev, dtype=torch.float8_e5m2):
     return torch.from_numpy(np.ascontiguousarray(packed)).view(dtype).to(dev)
+
+
+def torch_ref_dev(a, bp, scale, bias, out_dtype, b_dtype=torch.float8_e5m2):
+    """Whole-output reference on the device for full-size shapes, in the oracle's formulation
+    (scaled_mm_ref): the fp16 activations times the decoded weight summed in float64 (every
+    product is exact), rounded to float32, the scale applied in float32, one rounding to the
+    output type, the bias added in the output type."""
+    k16, N, _ = bp.shape
+    dec = bp.view(b_dtype).double().permute(0, 2, 1).reshape(k16 * 16, N)
+    acc = (a.double() @ dec).float()
+    del dec
+    if scale is not None:
+        acc.mul_(scale.float().reshape(()))
+    y = acc.to(out_dtype)
+    del acc
+    if bias is not None:
+        y = (y.float() + bias.float()).to(out_dtype)
+    return y
+
+
+def assert_gemm_close_dev(out, ref, out_dtype, label=""):
+    """assert_gemm_close's gate evaluated on the device over the whole output (same bounds)."""
+    o = out.double()
+    r = ref.double()
+    assert torch.equal(torch.isnan(o), torch.isnan(r)), f"{label}: NaN pattern differs"
+    inf = torch.isinf(r)
+    assert torch.equal(o[inf], r[inf]), f"{label}: inf pattern differs"
+    fin = torch.isfinite(r)
+    o, r = o[fin], r[fin]
+    d = (o - r).abs()
+    mant = 10 if out_dtype == torch.float16 else 7
+    ulp = torch.exp2(torch.floor(torch.log2(r.abs().clamp_min(2.0 ** -14))) - mant)
+    tol = torch.clamp(2.0 * ulp * 1.0001, min=2e-2)
+    fro = (d.norm() / r.norm().clamp_min(1e-6)).item()
+    ratio = d / tol
+    worst = ratio.max().item() if d.numel() else 0.0
+    assert fro <= 1e-3, f"{label}: rel-Fro {fro:.3g} > 1e-3"
+    if worst > 1.0:
+        i = int(ratio.argmax())
+        flat = fin.nonzero()[i].tolist()
+        raise AssertionError(f"{label}: max |diff|/tol = {worst:.3g} at {flat}: got {o[i].item()!r}, "
+                             f"want {r[i].item()!r}")
+    return fro
+
+
+def assert_row_col_checksums(a, bp, scale, bias, y, b_dtype=torch.float8_e5m2, label=""):
+    """Size-independent check of the whole output against float64 arithmetic (no torch matmul
+    in fp32): the row sums of C equal A @ (dec(B) @ 1) * s + sum(bias) and its column sums equal
+    (1ᵀA) @ dec(B) * s + M * bias, within the sum of the per-element bounds: two output ulps
+    (two roundings) plus 8·sqrt(K)·2^-24·|a_m|·|b_n|·|s| for the fp32 sum (a probabilistic bound
+    on rounding errors, Higham §2.8). A wrong, missing or misplaced output tile moves a sum by
+    far more."""
+    k16, N, _ = bp.shape
+    K = k16 * 16
+    M = a.shape[0]
+    dec = bp.view(b_dtype).double().permute(0, 2, 1).reshape(K, N)
+    a64 = a.double()
+    s = 1.0 if scale is None else float(scale.reshape(()).item())
+    b64 = torch.zeros(N, dtype=torch.float64, device=a.device) if bias is None else bias.double()
+    y64 = y.double()
+    mant = 10 if y.dtype == torch.float16 else 7
+    elem = 2.0 * torch.exp2(torch.floor(torch.log2(y64.abs().clamp_min(2.0 ** -14))) - mant)
+    an = a64.norm(dim=1)  # |a_m|
+    bn = dec.norm(dim=0) * abs(s)  # |b_n| * |s|
+    c = 8.0 * K ** 0.5 * 2.0 ** -24
+    row_tol = elem.sum(1) + c * an * bn.sum() + 1e-6
+    row_d = ((y64.sum(1) - (a64 @ dec.sum(1)) * s - b64.sum())).abs()
+    assert bool((row_d <= row_tol).all()), f"{label}: row checksum off by {(row_d / row_tol).max().item():.3g}x its bound"
+    col_tol = elem.sum(0) + c * an.sum() * bn + 1e-6
+    col_d = (y64.sum(0) - (a64.sum(0) @ dec) * s - M * b64).abs()
+    assert bool((col_d <= col_tol).all()), f"{label}: column checksum off by {(col_d / col_tol).max().item():.3g}x its bound"

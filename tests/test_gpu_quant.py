@@ -246,3 +246,24 @@ def test_capi_quantize_workspace_reused_across_shapes(cuda):
         codes, s_ref = O.quantize_native(w.numpy(), O.DT_F16)
         assert np.float32(scale.item()) == s_ref, f"{N}x{K}"
         assert np.array_equal(O.unprepack_transpose(out.cpu().numpy()), codes), f"{N}x{K}"
+
+
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_load_path_e5m2_checkpoint(cuda, quant, with_scale):
+    """An e5m2 checkpoint is only prepacked (reference quant.py:120-126): the codes pass through
+    unchanged, the scale is the checkpoint's weight_scale as fp32, or 1 when there is none."""
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(384, 512, generator=g) * 3.0).to(torch.float8_e5m2)
+    codes = w.view(torch.uint8).numpy()
+    ck = torch.tensor(0.0123, dtype=torch.bfloat16) if with_scale else None
+    qt = quant.make_feather_quantized_weight(w.to(cuda), None if ck is None else ck.to(cuda), torch.bfloat16)
+    qdata, scale = quant.get_feather_plain_tensors(qt)
+    assert qdata.dtype == torch.float8_e5m2 and qdata.shape == (32, 384, 16) and qdata.device == cuda
+    assert np.array_equal(_bytes(qdata), O.prepack_transpose(codes))
+    assert scale.dtype == torch.float32 and scale.device == cuda
+    assert scale.item() == (np.float32(ck.float().item()) if with_scale else 1.0)
+    assert qt.params.orig_dtype == torch.bfloat16 and qt.params.orig_shape == (384, 512)
+    # the layout's dequantize undoes it: code value times the scale, in orig_dtype
+    deq = qt.dequantize()
+    ref = O.dequantize(codes, np.float32(scale.item()), O.DT_BF16)
+    assert np.array_equal(deq.view(torch.int16).cpu().numpy().view(np.uint16), ref)

@@ -6,7 +6,8 @@ import pytest
 import torch
 
 from conftest import GOLDEN
-from gpu_util import assert_gemm_close, capi_scaled_mm, lib, stream, to_dev_codes, weight_like
+from gpu_util import (assert_gemm_close, assert_gemm_close_dev, assert_row_col_checksums, capi_scaled_mm, lib,
+                      stream, to_dev_codes, torch_ref_dev, weight_like)
 from oracle import feather_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -187,6 +188,11 @@ def _sampled_rows_check(cuda, M, N, K, out_dtype, cfg, nrows=24, seed=0):
     ref = O.scaled_mm_ref(a[torch.from_numpy(rows).to(cuda)].cpu().numpy(), packed, s, bias_np, od)
     assert_gemm_close(y[torch.from_numpy(rows).to(cuda)], ref, out_dtype, f"{M}x{N}x{K}")
     assert torch.isfinite(y).all()
+    # the whole output: elementwise against a torch fp32 matmul of the same operands, and row and
+    # column checksums against float64 arithmetic
+    bd, sd, bsd = to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), bias.to(cuda)
+    assert_gemm_close_dev(y, torch_ref_dev(a, bd, sd, bsd, out_dtype), out_dtype, f"full {M}x{N}x{K}")
+    assert_row_col_checksums(a, bd, sd, bsd, y, label=f"{M}x{N}x{K}")
 
 
 def test_baseline_config2_small_m(cuda):
@@ -418,3 +424,46 @@ def test_every_fp8_code_decodes_exactly(cuda, b_dtype, route):
     assert torch.equal(torch.isnan(got), torch.isnan(want)), route
     fin = ~torch.isnan(want)
     assert torch.equal(got[fin], want[fin]), route
+
+
+def test_baseline_config1_gemm(cuda, hk, quant):
+    """BASELINE config 1 end to end: A (256,1024) ~N(0,1) fp16, W (1024,1024) ~N(0,0.02) in fp16
+    quantized on the load path (its bytes and scale equal the golden fixture), fp16 out with a
+    bias; the GEMM through the C ABI on every config tuple that takes M=256, through the
+    reference's torch op and through the drop-in Python entries, each against the oracle over
+    the whole output."""
+    z = np.load(GOLDEN / "quant_c1.npz")
+    g = torch.Generator().manual_seed(0)
+    w32 = torch.randn(1024, 1024, generator=g) * 0.02  # the golden fixture's weight
+    a = torch.randn(256, 1024, generator=g).half()
+    bias = (torch.randn(1024, generator=g) * 0.01).half()
+    qt = quant.make_feather_quantized_weight(w32.half().to(cuda), None, torch.float16)
+    bp, sd = quant.get_feather_plain_tensors(qt)
+    assert np.float32(sd.item()) == z["load_f16_scale"][0]
+    import hashlib
+
+    packed = bp.view(torch.uint8).cpu().numpy()
+    assert hashlib.sha256(packed.tobytes()).digest() == z["load_f16_sha256"].tobytes()
+    ad, bsd = a.to(cuda), bias.to(cuda)
+    sd = sd.reshape(1).contiguous()
+    ref = O.scaled_mm_ref(a.numpy(), packed, np.float32(sd.item()), bias.numpy(), O.DT_F16)
+    ran = 0
+    for cfg in hk._CONFIGS:
+        wm, wn, u, rm, rn = cfg
+        if 256 % (16 * wm * rm) or 1024 % (16 * wn * rn) or 1024 % (16 * u):
+            continue
+        print("C1 cfg", cfg, flush=True)
+        y = capi_scaled_mm(ad, bp, sd, bsd, torch.float16, cfg)
+        assert_gemm_close(y, ref, torch.float16, f"C1 capi {cfg}")
+        ran += 1
+    assert ran >= 20
+    c = torch.empty(256, 1024, dtype=torch.float16, device=cuda)
+    torch.ops.feather_ops.scaled_mm(ad, bp, sd, bsd, c, 2, 4, 4, 8, 4, 1)
+    torch.cuda.synchronize()
+    assert_gemm_close(c, ref, torch.float16, "C1 torch op")
+    y = hk.scaled_mm_hip(ad, bp, sd, bsd, torch.float16)
+    assert_gemm_close(y, ref, torch.float16, "C1 scaled_mm_hip")
+    y = hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16)
+    assert_gemm_close(y, ref, torch.float16, "C1 any-M")
+    # the route BASELINE config 1 takes by default (split-K 64x64 tiles) is deterministic
+    assert torch.equal(y, hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16))

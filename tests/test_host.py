@@ -237,3 +237,54 @@ def test_small_m_plan_workspace(pkg):
     # 80 strips of 64 columns x 3 K ranges: the fixed 64 KB counter region + 3 fp32 partial tiles per strip
     assert lib.feather_scaled_mm_workspace_size(16, 5120, 13824, *cfg) == 65536 + 80 * 3 * 16 * 64 * 4
     assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 65536 + 48 * 4 * 1 * 64 * 4
+
+
+def test_packed_params_protocol(quant):
+    """FeatherFP8E5M2PackedParams (reference comfy_feather/quant.py:22-49): to_device and clone
+    return new params with their own scale tensor; copy_from updates in place, keeping the
+    scale's storage."""
+    P = quant.FeatherFP8E5M2PackedParams
+    p = P(scale=torch.tensor(0.5), orig_dtype=torch.float16, orig_shape=(8, 16))
+    assert p._tensor_fields() == ["scale"]
+    c = p.clone()
+    assert c.scale.data_ptr() != p.scale.data_ptr() and c.scale.item() == 0.5
+    d = p.to_device("cpu")
+    assert d.scale.item() == 0.5 and d.orig_dtype == torch.float16 and d.orig_shape == (8, 16)
+    src = P(scale=torch.tensor(2.0), orig_dtype=torch.bfloat16, orig_shape=(4, 32))
+    ptr = p.scale.data_ptr()
+    p.copy_from(src)
+    assert p.scale.data_ptr() == ptr and p.scale.item() == 2.0
+    assert p.orig_dtype == torch.bfloat16 and p.orig_shape == (4, 32)
+
+
+def test_capi_rejects_shapes_past_offset_limits(pkg):
+    """K >= 2^22 or N >= 2^25 would overflow the LDS kernels' 32-bit per-lane copy offsets:
+    refused before any launch (kernel id 0, launch returns false)."""
+    from featherops_amd.kernel.hip import _lib
+
+    L = _lib.lib()
+    cfg = (2, 4, 4, 8, 4)
+    assert L.feather_scaled_mm_kernel_id(256, 16, (1 << 22) - 16, *cfg) != 0
+    assert L.feather_scaled_mm_kernel_id(256, 16, 1 << 22, *cfg) == 0
+    assert L.feather_scaled_mm_kernel_id(256, (1 << 25) - 16, 16, *cfg) != 0
+    assert L.feather_scaled_mm_kernel_id(256, 1 << 25, 16, *cfg) == 0
+    assert not L.launch_scaled_mm(None, None, None, None, None, 256, 16, 1 << 22, 0, 0, *cfg, 1, 0, None)
+
+
+def test_splitk_plan_without_counter_room_needs_no_workspace():
+    """A split-K tile plan with more output tiles than the 16384 arrival counters runs
+    unsplit: it asks for no workspace (run in a fresh process, the workgroup target is read
+    once)."""
+    import subprocess
+    import sys
+
+    code = ("import __graft_entry__; __graft_entry__.load_package();"
+            "from featherops_amd.kernel.hip import _lib; L = _lib.lib();"
+            "print(L.feather_scaled_mm_workspace_size(64, 16400 * 64, 512, 2, 2, 4, 4, 4),"
+            " L.feather_scaled_mm_workspace_size(64, 4096, 4096, 2, 2, 4, 4, 4))")
+    env = dict(__import__("os").environ, FEATHEROPS_SMALLM_GROUPS="40000")
+    out = subprocess.run([sys.executable, "-c", code], cwd=REPO, env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    big, small = map(int, out.stdout.split())
+    assert big == 0 and small > 0

@@ -26,6 +26,32 @@ def test_e5m2_decode_exhaustive_vs_torch():
     assert np.array_equal(t[~np.isnan(t)], o[~np.isnan(o)])
 
 
+def test_e4m3fn_decode_exhaustive_vs_torch():
+    # reference kernel/hip/hip_kernel.py:37 routes float8_e4m3fn weights to the same GEMM and
+    # test_scaled_mm_hip.py:53-54 builds them with torch's cast: torch's decode is the ground truth
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    o = O.e4m3fn_decode(codes)
+    assert np.array_equal(np.isnan(t), np.isnan(o))
+    assert np.array_equal(np.isnan(o).nonzero()[0], [0x7F, 0xFF])
+    fin = ~np.isnan(t)
+    assert np.array_equal(t[fin].view(np.uint32), o[fin].view(np.uint32))  # signed zeros included
+
+
+def test_e4m3fn_known_answers():
+    # values fixed by the OCP fp8 definition: max normal 448, min normal 2^-6, min subnormal 2^-9
+    kat = {0x00: 0.0, 0x38: 1.0, 0xB8: -1.0, 0x7E: 448.0, 0xFE: -448.0, 0x08: 2.0**-6,
+           0x01: 2.0**-9, 0x07: 7 * 2.0**-9, 0x3C: 1.5, 0x40: 2.0, 0x30: 0.5}
+    for code, val in kat.items():
+        assert O.e4m3fn_decode(np.array([code], np.uint8))[0] == val
+    # the encode direction through torch round-trips every finite code
+    codes = np.arange(256, dtype=np.uint8)
+    vals = O.e4m3fn_decode(codes)
+    fin = ~np.isnan(vals)
+    back = torch.from_numpy(vals[fin]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(back, codes[fin])
+
+
 def test_e5m2_known_answers():
     # cpp_benchmarks/benchmark_scaled_mm_hip.cpp:127-137 of the reference
     kat = {0xBC: -1.0, 0xBA: -0.75, 0xB8: -0.5, 0xB4: -0.25, 0x00: 0.0, 0x34: 0.25, 0x38: 0.5, 0x3A: 0.75, 0x3C: 1.0}
