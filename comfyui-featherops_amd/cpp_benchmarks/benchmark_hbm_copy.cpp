@@ -8,10 +8,12 @@
 //       67 MB and 268 MB buffers, cycling 24 buffers so that the 256 MB
 //       Infinity Cache cannot serve them: the per-call floor a weight-streaming
 //       kernel of that size can reach (launch + ramp + drain included)
+//   benchmark_hbm_copy --read-bytes B  the same floor for one size of B bytes
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 #include <cstdlib>
+#include <initializer_list>
 #include <iostream>
 #include <string>
 
@@ -43,14 +45,15 @@ __global__ __launch_bounds__(256) void read16(const uint4* __restrict__ src, int
     if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live
 }
 
-int read_sweep() {
+int read_sweep(const std::initializer_list<int64_t>& sizes) {
     const int nbuf = 24;
     uint32_t* sink;
     HIP_OK(hipMalloc(&sink, 4));
     hipEvent_t t0, t1;
     HIP_OK(hipEventCreate(&t0));
     HIP_OK(hipEventCreate(&t1));
-    for (const int64_t bytes : {int64_t(16777216), int64_t(67108864), int64_t(268435456)}) {
+    for (const int64_t bytes0 : sizes) {
+        const int64_t bytes = (bytes0 + 15) / 16 * 16;
         void* bufs[nbuf];
         for (auto& b : bufs) {
             HIP_OK(hipMalloc(&b, bytes));
@@ -81,7 +84,15 @@ int main(int argc, char** argv) {
     int iters = 20;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
-        if (a == "--read-sweep") return read_sweep();
+        if (a == "--read-sweep") return read_sweep({int64_t(16777216), int64_t(67108864), int64_t(268435456)});
+        if (a == "--read-bytes" && i + 1 < argc) {
+            const int64_t b = std::stoll(argv[++i]);
+            if (b <= 0 || b > (int64_t(1) << 32)) {
+                std::cerr << "--read-bytes takes 1 .. 2^32" << std::endl;
+                return 1;
+            }
+            return read_sweep({b});
+        }
         if (i + 1 >= argc) break;
         if (a == "--mib") mib = std::stoll(argv[++i]);
         else if (a == "--iters") iters = std::stoi(argv[++i]);

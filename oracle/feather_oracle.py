@@ -349,3 +349,23 @@ def e4m3fn_decode(codes: np.ndarray) -> np.ndarray:
     val = np.where(e == 0, (m / 8.0) * 2.0**-6, (1.0 + m / 8.0) * np.power(2.0, e - 7))
     val = np.where((c & 0x7F) == 0x7F, np.nan, val)
     return (s * val).astype(np.float32)
+
+
+def scaled_mm_naive_torch(a, b_prepacked, scale, bias, out_dtype):
+    """kernel/naive.py:4-41 (b_prepacked=True, per-tensor scale) on host torch, for the CPU
+    baseline: the (K/16, N, 16) codes are unpacked to (K, N) and decoded to fp16, the product is
+    torch's fp16 CPU matmul (rounded to fp16, naive.py:20-23), then scale in fp32, cast to
+    out_dtype, bias added in out_dtype. a: fp16 (M, K) tensor; b_prepacked: uint8 or fp8
+    (K/16, N, 16) tensor; scale: 0-d/1-element fp32 tensor or None; bias: (N,) tensor or None."""
+    import torch
+
+    k16, n, _ = b_prepacked.shape
+    codes = b_prepacked.view(torch.uint8).transpose(1, 2).reshape(k16 * 16, n)
+    w16 = codes.view(torch.float8_e5m2).to(torch.float16)
+    prod = torch.matmul(a.to(torch.float16), w16)
+    if scale is not None:
+        prod = prod.float() * scale.float().reshape(())
+    y = prod.to(out_dtype)
+    if bias is not None:
+        y = y + bias.to(out_dtype)
+    return y

@@ -271,3 +271,24 @@ def test_golden_fixtures_match_oracle():
     gm = np.load(GOLDEN / "gemm_small.npz")
     y = O.scaled_mm_ref(gm["a"], gm["b_prepacked"], gm["scale"][0], gm["bias_f16"], O.DT_F16)
     assert np.array_equal(y, gm["out_f16"])
+
+
+def test_naive_torch_matches_numpy_naive():
+    """The host-torch restatement of kernel/naive.py (the CPU baseline) against the numpy one:
+    both round A @ B to fp16 before the scale; torch's fp16 CPU matmul sums in another order,
+    so they agree to the fp16 rounding of the product, not bit for bit. A wrong unpack or a
+    transposed operand would be off by O(1)."""
+    g = torch.Generator().manual_seed(3)
+    for M, N, K in [(64, 128, 256), (256, 1024, 1024), (33, 80, 4096)]:
+        a = torch.randn(M, K, generator=g).half()
+        w = (torch.randn(K, N, generator=g) * 0.05).to(torch.float8_e5m2).view(torch.uint8).numpy()
+        packed = O.prepack_kn(w)
+        s = np.float32(0.75)
+        bias = (torch.randn(N, generator=g) * 0.01).half()
+        y = O.scaled_mm_naive_torch(a, torch.from_numpy(packed), torch.tensor(s), bias, torch.float16)
+        r = O.scaled_mm_naive(a.numpy(), packed, s, bias.numpy(), O.DT_F16).astype(np.float32)
+        assert y.dtype == torch.float16 and y.shape == (M, N)
+        y = y.float().numpy()
+        assert np.allclose(y, r, rtol=2e-3, atol=1e-3 * np.abs(r).max())
+        ref = O.scaled_mm_ref(a.numpy(), packed, s, bias.numpy(), O.DT_F16).astype(np.float32)
+        assert np.allclose(y, ref, rtol=2e-3, atol=1e-3 * np.abs(ref).max())
