@@ -4,6 +4,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "featherops_amd.h"
 #include "quant_prepack.h"
 #include "scaled_mm_dispatch.h"
@@ -132,6 +134,48 @@ int device_cus() {
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FEATHER_OK : FEATHER_ERR_LAUNCH; }
 
+// ---- allocation-free K-split scratch (feather_launch_scaled_mm_noalloc) ----
+// One static device array per GPU holds what a caller workspace holds for the
+// K split: the 64 KB arrival-counter region, then fp32 partial tiles. The
+// loader zero-fills it; every call leaves the counters at zero again. In host
+// code `scratch` names a host-side stand-in, never the device memory: its
+// device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoallocScratchBytes = FEATHER_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoallocScratchBytes > feather::kWorkspaceCounterBytes, "scratch holds the counter region");
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device; the first call on a
+// device looks it up and clears the counter region (a fill kernel on `stream`,
+// ordered before the call's GEMM).
+int noalloc_scratch(void** out, hipStream_t stream) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return FEATHER_ERR_INVALID;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            (void)hipGetLastError();
+            return FEATHER_ERR_LAUNCH;
+        }
+        constexpr int kWords = static_cast<int>(feather::kWorkspaceCounterBytes / 4);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((kWords + 255) / 256), dim3(256), 0, stream,
+                           static_cast<uint32_t*>(ptr), kWords);
+        if (hipGetLastError() != hipSuccess) return FEATHER_ERR_LAUNCH;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return FEATHER_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -231,6 +275,27 @@ bool feather_launch_scaled_mm_ws(const void* a, const uint8_t* b_prepacked, cons
     return feather_launch_scaled_mm_ex(a, FEATHER_DTYPE_F16, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias,
                                        block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
                                        output_dtype, workspace, workspace_bytes, stream);
+}
+
+int feather_launch_scaled_mm_noalloc(const void* a, int a_dtype, const uint8_t* b_prepacked, const float* scale,
+                                     const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale,
+                                     int has_bias, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m,
+                                     int repeat_n, int b_dtype, int output_dtype, hipStream_t stream) {
+    const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    if (kid == feather::kKernelNone) return FEATHER_ERR_UNSUPPORTED;
+    const size_t need =
+        feather_scaled_mm_workspace_size(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
+    if (need > kNoallocScratchBytes) return FEATHER_ERR_SCRATCH;
+    void* ws = nullptr;
+    if (need > 0 && M > 0) {
+        const int st = noalloc_scratch(&ws, stream);
+        if (st != FEATHER_OK) return st;
+    }
+    if (!feather_launch_scaled_mm_ex(a, a_dtype, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias,
+                                     block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, b_dtype,
+                                     output_dtype, ws, ws ? kNoallocScratchBytes : 0, stream))
+        return FEATHER_ERR_UNSUPPORTED;
+    return launch_status();
 }
 
 bool launch_scaled_mm(const void* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias, uint16_t* c,
@@ -351,6 +416,7 @@ const char* feather_status_string(int status) {
         case FEATHER_ERR_INVALID: return "invalid argument";
         case FEATHER_ERR_UNSUPPORTED: return "unsupported configuration";
         case FEATHER_ERR_LAUNCH: return "kernel launch failed";
+        case FEATHER_ERR_SCRATCH: return "call needs more K-split scratch than the static array holds";
         default: return "unknown status";
     }
 }

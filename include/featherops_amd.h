@@ -31,6 +31,10 @@ extern "C" {
 #define FEATHER_ERR_INVALID 1      /* argument out of the supported domain */
 #define FEATHER_ERR_UNSUPPORTED 2  /* no kernel for this configuration */
 #define FEATHER_ERR_LAUNCH 3       /* hipGetLastError() reported a launch failure */
+#define FEATHER_ERR_SCRATCH 4      /* the call needs more scratch than FEATHER_NOALLOC_SCRATCH_BYTES */
+
+/* Size of the static per-GPU scratch array of feather_launch_scaled_mm_noalloc (16 MiB). */
+#define FEATHER_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 /* Data type codes. */
 #define FEATHER_DTYPE_F16 0
@@ -101,6 +105,29 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
                                  int has_bias, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m,
                                  int repeat_n, int b_dtype, int output_dtype, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
+
+/*
+ * feather_launch_scaled_mm_ex without a workspace argument and without any
+ * allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. The K-split scratch (arrival
+ * counters and fp32 partials) is a static device array of
+ * FEATHER_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the
+ * first call on a device looks up its address (hipGetSymbolAddress) and
+ * clears its counters with a fill kernel on `stream`. Results equal
+ * feather_launch_scaled_mm_ex with a caller workspace of the size
+ * feather_scaled_mm_workspace_size reports. Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller. Returns FEATHER_OK,
+ * FEATHER_ERR_UNSUPPORTED (no kernel for this configuration / activation
+ * dtype, nothing launched), FEATHER_ERR_SCRATCH (the call's K split needs more
+ * than the array holds, nothing launched), FEATHER_ERR_INVALID or
+ * FEATHER_ERR_LAUNCH.
+ */
+int feather_launch_scaled_mm_noalloc(const void* a, int a_dtype, const uint8_t* b_prepacked, const float* scale,
+                                     const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale,
+                                     int has_bias, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m,
+                                     int repeat_n, int b_dtype, int output_dtype, hipStream_t stream);
 
 /*
  * feather_launch_scaled_mm_ws with the unmerged-LoRA term fused into the
