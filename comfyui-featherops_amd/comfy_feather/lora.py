@@ -8,7 +8,8 @@ Two forms:
   * apply_lora_patches(x, y, weight_functions): the reference's separate pass,
     y += F.linear(F.linear(x, down), up) * s per patch;
   * lora_factors(x, weight_functions): the factors of the same term for the
-    GEMM's fused epilogue -- T = F.linear(x, [down_i * s_i]_i) (M, R) and
+    GEMM's fused epilogue -- T = F.linear(x, [down_i * s_i]_i) (M, R), computed
+    by the library's down-projection kernel (lora_down), and
     U = [up_i]_i (N, R), stacked over the patches along the rank and
     zero-padded to a multiple of 32, in x's dtype. The GEMM then adds T . U^T
     to its fp32 accumulator before rounding, so C is written once.
@@ -16,6 +17,8 @@ Two forms:
 
 import torch
 import torch.nn.functional as F
+
+from ..kernel.hip import _lib
 
 
 def _basic_patches(weight_functions):
@@ -92,4 +95,16 @@ def lora_factors(x: torch.Tensor, weight_functions, cache: dict | None = None):
         else:
             d, u = _stacked_factors(x, patches)
             cache["entry"] = (key, [(dn, up) for dn, up, _ in patches], d, u)
-    return F.linear(x, d).contiguous(), u
+    return lora_down(x, d), u
+
+
+def lora_down(x: torch.Tensor, d: torch.Tensor) -> torch.Tensor:
+    """T = F.linear(x, d) on the library's skinny-GEMM kernel (torch.ops.feather_ops.lora_down:
+    fp32 accumulation, rounded to x's dtype); torch's F.linear only when K is not a multiple of 8
+    (the kernel's 16-byte row loads) or x is not on the GPU."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.is_cuda and x2.shape[1] % 8 == 0 and d.shape[0] % 32 == 0:
+        _lib.load_torch_ops()
+        t = torch.ops.feather_ops.lora_down.default(x2.contiguous(), d.contiguous())
+        return t.reshape(*x.shape[:-1], d.shape[0])
+    return F.linear(x, d).contiguous()

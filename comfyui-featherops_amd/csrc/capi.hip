@@ -7,6 +7,7 @@
 #include <mutex>
 
 #include "featherops_amd.h"
+#include "lora_down.h"
 #include "quant_prepack.h"
 #include "scaled_mm_dispatch.h"
 
@@ -407,6 +408,33 @@ int feather_dequantize_e5m2(const uint8_t* packed, const float* scale, void* out
     if ((reinterpret_cast<uintptr_t>(packed) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u))
         return FEATHER_ERR_INVALID;
     feather::launch_dequant(packed, scale, out, N, K, out_dtype, stream);
+    return launch_status();
+}
+
+size_t feather_lora_down_workspace_size(int64_t M, int64_t K, int64_t R) {
+    if (M <= 0 || K <= 0 || R <= 0 || R % 32 != 0) return 0;
+    return feather::lora_down_workspace_bytes(M, K, R);
+}
+
+int feather_lora_down(const void* x, int x_dtype, const void* d, void* t, int64_t M, int64_t K, int64_t R,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (x_dtype != FEATHER_DTYPE_F16 && x_dtype != FEATHER_DTYPE_BF16) return FEATHER_ERR_INVALID;
+    if (M < 0 || K <= 0 || R <= 0 || M > INT32_MAX || R > 65536) return FEATHER_ERR_INVALID;
+    // per-lane copy offsets within a tile (up to 128 rows of D) are 32-bit: 128 * K * 2 < 2^32
+    if (K % 8 != 0 || R % 32 != 0 || K >= (int64_t{1} << 24)) return FEATHER_ERR_UNSUPPORTED;
+    if (M == 0) return FEATHER_OK;
+    if (!x || !d || !t) return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(t)) % 16 != 0)
+        return FEATHER_ERR_INVALID;
+    feather::LoraDownArgs a;
+    a.x = static_cast<const uint16_t*>(x);
+    a.d = static_cast<const uint16_t*>(d);
+    a.t = static_cast<uint16_t*>(t);
+    a.M = M;
+    a.K = K;
+    a.R = R;
+    a.bf16 = x_dtype == FEATHER_DTYPE_BF16;
+    feather::launch_lora_down(a, workspace, workspace_bytes, stream);
     return launch_status();
 }
 

@@ -10,6 +10,8 @@
 //                                 fused into the epilogue on the large tiles
 //   feather_ops::quantize_prepack_e5m2(_scaled)
 //                                 the fused quantize + prepack of a weight
+//   feather_ops::lora_down        T = F.linear(x, d), the LoRA down-projection
+//                                 of all patches at once
 //   feather_ops_internal::scaled_mm_configured
 //                                 the reference's configured op (hip_kernel.py:
 //                                 12-58, a Python custom op there), Meta kernel
@@ -291,6 +293,35 @@ at::Tensor scaled_mm_any_m_lora_meta(const at::Tensor& a, const at::Tensor& b_pr
     return at::empty({a.size(0), b_prepacked.size(1)}, a.options().dtype(out_dtype));
 }
 
+// feather_ops::lora_down: T = F.linear(x, d) for the fused LoRA epilogue (the first
+// F.linear of the reference's comfy_feather/lora.py:4-35, all patches stacked
+// along the rank): x (M, K) and d (R, K) contiguous in the same dtype (fp16 or
+// bf16), K % 8 == 0, R % 32 == 0; T (M, R) in that dtype, fp32 accumulation.
+at::Tensor lora_down(const at::Tensor& x, const at::Tensor& d) {
+    TORCH_CHECK(x.is_cuda() && d.is_cuda() && d.device() == x.device(), "x and d must be CUDA tensors on one device");
+    TORCH_CHECK(x.dim() == 2 && d.dim() == 2 && x.size(1) == d.size(1), "x must be (M, K) and d (R, K)");
+    TORCH_CHECK(x.scalar_type() == d.scalar_type() &&
+                    (x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16),
+                "x and d must both be float16 or both bfloat16");
+    TORCH_CHECK(x.is_contiguous() && d.is_contiguous(), "x and d must be contiguous");
+    const int64_t M = x.size(0), K = x.size(1), R = d.size(0);
+    TORCH_CHECK(K % 8 == 0 && R > 0 && R % 32 == 0, "lora_down needs K % 8 == 0 and R a positive multiple of 32");
+    at::Tensor t = at::empty({M, R}, x.options());
+    if (M == 0) return t;
+    const c10::DeviceGuard guard(x.device());
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    const size_t ws_bytes = feather_lora_down_workspace_size(M, K, R);
+    void* ws = ws_bytes ? workspace_for(x.device(), stream, ws_bytes).data_ptr() : nullptr;
+    const int st = feather_lora_down(x.data_ptr(), x.scalar_type() == at::kHalf ? FEATHER_DTYPE_F16 : FEATHER_DTYPE_BF16,
+                                     d.data_ptr(), t.data_ptr(), M, K, R, ws, ws_bytes, stream);
+    TORCH_CHECK(st == FEATHER_OK, "feather_lora_down failed: ", feather_status_string(st));
+    return t;
+}
+
+at::Tensor lora_down_meta(const at::Tensor& x, const at::Tensor& d) {
+    return at::empty({x.size(0), d.size(0)}, x.options());
+}
+
 int weight_dtype_code(const at::Tensor& w) {
     switch (w.scalar_type()) {
         case at::kHalf: return FEATHER_DTYPE_F16;
@@ -370,6 +401,7 @@ TORCH_LIBRARY(feather_ops, m) {
           "Tensor lora_t, Tensor lora_u) -> Tensor");
     m.def("quantize_prepack_e5m2(Tensor w, Tensor? ckpt_scale, bool native) -> (Tensor, Tensor)");
     m.def("quantize_prepack_e5m2_scaled(Tensor w, Tensor scale) -> Tensor");
+    m.def("lora_down(Tensor x, Tensor d) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
@@ -378,11 +410,13 @@ TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora);
     m.impl("quantize_prepack_e5m2", &quantize_prepack_e5m2);
     m.impl("quantize_prepack_e5m2_scaled", &quantize_prepack_e5m2_scaled);
+    m.impl("lora_down", &lora_down);
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, Meta, m) {
     m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta);
     m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora_meta);
+    m.impl("lora_down", &lora_down_meta);
 }
 
 // the reference's Python custom op of this name, as a C++ op (the namespace

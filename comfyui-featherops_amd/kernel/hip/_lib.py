@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple] = {
                                                 _int, _int, _int, _int, _int, _int, _vp]),
     "feather_launch_scaled_mm_lora": (ctypes.c_bool, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp,
                                                       _i64, _int, _int, _int, _int, _int, _int, _int, _int, _vp]),
+    "feather_lora_down": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp]),
+    "feather_lora_down_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "feather_scaled_mm_pick_config": (_int, [_i64, _i64, _i64, ctypes.POINTER(ctypes.c_int)]),
     "feather_scaled_mm_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "feather_scaled_mm_kernel_id": (_int, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),

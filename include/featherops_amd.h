@@ -150,6 +150,26 @@ bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, co
                                    int b_dtype, int output_dtype, hipStream_t stream);
 
 /*
+ * LoRA down-projection T = x . D^T: x (M, K) and D (R, K) row-major in the
+ * same dtype (x_dtype FEATHER_DTYPE_F16 or _BF16), T (M, R) in that dtype,
+ * fp32 accumulation rounded to nearest-even -- the F.linear(x, lora_A) that
+ * starts the reference's side path (comfy_feather/lora.py:27), for every
+ * patch at once when the down matrices are stacked along the rank (the T
+ * argument of feather_launch_scaled_mm_lora). K % 8 == 0, K < 2^24 and
+ * R % 32 == 0 (else FEATHER_ERR_UNSUPPORTED, nothing launched), 16-byte
+ * aligned buffers. For small M the kernel also splits K across workgroups
+ * through `workspace` (same contract as feather_launch_scaled_mm_ws: first
+ * 64 KB arrival counters, zero before the first call and left zero by every
+ * call; a workspace smaller than feather_lora_down_workspace_size, or NULL,
+ * runs unsplit with the same result). Returns a status code.
+ */
+int feather_lora_down(const void* x, int x_dtype, const void* d, void* t, int64_t M, int64_t K, int64_t R,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes feather_lora_down can use for this call (0 = none). */
+size_t feather_lora_down_workspace_size(int64_t M, int64_t K, int64_t R);
+
+/*
  * A configuration tuple for this shape on the current device, without timing
  * anything: the output tile whose waves of workgroups times tile cost is
  * smallest (256x256, 256x192, 128x256, 256x128 or 128x128; the small-M

@@ -369,3 +369,19 @@ def scaled_mm_naive_torch(a, b_prepacked, scale, bias, out_dtype):
     if bias is not None:
         y = y + bias.to(out_dtype)
     return y
+
+
+def lora_down_ref(x: np.ndarray, d: np.ndarray, dtype: str) -> np.ndarray:
+    """T = F.linear(x, lora_A), the first step of the reference's LoRA side path
+    (comfy_feather/lora.py:27-30): x (M, K) and d (R, K) in dtype (float16 arrays,
+    or uint16 bf16 bits), the products summed in float64, rounded to float32 and
+    then to dtype (nearest even). Returns float16 for f16, uint16 bf16 bits for bf16."""
+    if dtype == DT_F16:
+        x64 = np.asarray(x, dtype=np.float16).astype(np.float64)
+        d64 = np.asarray(d, dtype=np.float16).astype(np.float64)
+    else:
+        x64 = bf16_bits_to_f32(np.asarray(x, dtype=np.uint16)).astype(np.float64)
+        d64 = bf16_bits_to_f32(np.asarray(d, dtype=np.uint16)).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        acc = (x64 @ d64.T).astype(np.float32)
+    return f32_to_fp16_rne(acc) if dtype == DT_F16 else f32_to_bf16_rne(acc)

@@ -292,3 +292,36 @@ def test_naive_torch_matches_numpy_naive():
         assert np.allclose(y, r, rtol=2e-3, atol=1e-3 * np.abs(r).max())
         ref = O.scaled_mm_ref(a.numpy(), packed, s, bias.numpy(), O.DT_F16).astype(np.float32)
         assert np.allclose(y, ref, rtol=2e-3, atol=1e-3 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_lora_down_ref_brute_force_and_selection(dtype):
+    """lora_down_ref against explicit per-element loops on a tiny case, and a selection
+    matrix (d rows = unit vectors) that must return columns of x exactly."""
+    rng = np.random.default_rng(5)
+    M, K, R = 3, 16, 4
+    xf = rng.standard_normal((M, K)).astype(np.float32)
+    df = rng.standard_normal((R, K)).astype(np.float32)
+    if dtype == "f16":
+        x, d = xf.astype(np.float16), df.astype(np.float16)
+        xv, dv = x.astype(np.float64), d.astype(np.float64)
+    else:
+        x, d = O.f32_to_bf16_rne(xf), O.f32_to_bf16_rne(df)
+        xv, dv = O.bf16_bits_to_f32(x).astype(np.float64), O.bf16_bits_to_f32(d).astype(np.float64)
+    t = O.lora_down_ref(x, d, dtype)
+    for m in range(M):
+        for r in range(R):
+            s = 0.0
+            for k in range(K):
+                s += xv[m, k] * dv[r, k]
+            want = np.float32(s)
+            got = float(t[m, r]) if dtype == "f16" else float(O.bf16_bits_to_f32(np.array([t[m, r]]))[0])
+            want_r = float(np.float16(want)) if dtype == "f16" else float(
+                O.bf16_bits_to_f32(O.f32_to_bf16_rne(np.array([want], np.float32)))[0])
+            assert got == want_r
+    sel = np.zeros((K, K), np.float32)
+    sel[np.arange(K), rng.permutation(K)] = 1.0
+    ds = sel.astype(np.float16) if dtype == "f16" else O.f32_to_bf16_rne(sel)
+    cols = O.lora_down_ref(x, ds, dtype)
+    perm = sel.argmax(1)
+    assert np.array_equal(np.asarray(cols).view(np.uint16), np.asarray(x)[:, perm].view(np.uint16))
