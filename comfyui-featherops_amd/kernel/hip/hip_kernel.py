@@ -204,20 +204,55 @@ def _(a, b_prepacked, scale, bias, out_dtype, has_scale, has_bias, block_warps_m
     return torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
 
 
-def _torch_at_least(major: int, minor: int) -> bool:
-    parts = torch.__version__.split("+")[0].split(".")
-    return (int(parts[0]), int(parts[1])) >= (major, minor)
+def _autotune_decomposition(a, b_prepacked, scale, bias, **kw):
+    """What one Inductor autotuning choice of _autotuned_op runs: the configured op with that
+    choice's tuple. Inductor passes the op's non-tensor arguments by keyword: by name (the
+    lowering wrapper below names them), or as arg_<position> where a torch version's lowering
+    renames positional scalars itself; both spellings are read."""
+    out_dtype = kw["out_dtype"] if "out_dtype" in kw else kw["arg_4"]
+    has_scale = kw["has_scale"] if "has_scale" in kw else kw["arg_5"]
+    has_bias = kw["has_bias"] if "has_bias" in kw else kw["arg_6"]
+    cfg = (kw["block_warps_m"], kw["block_warps_n"], kw["unroll_k"], kw["repeat_m"], kw["repeat_n"])
+    return _configured_op(a, b_prepacked, scale if has_scale else None, bias if has_bias else None, out_dtype, *cfg)
 
 
-# Inductor's custom-op autotuning (the reference needs torch >= 2.12 for it,
-# README.md:46). Older inductors cannot bind this op's dtype argument during
-# autotuning, so there torch.compile runs the first compatible config.
-AUTOTUNE_UNDER_COMPILE = _torch_at_least(2, 12)
-if AUTOTUNE_UNDER_COMPILE:
-    from torch._inductor.kernel.custom_op import register_custom_op_autotuning
+# Inductor's custom-op autotuning (reference hip_kernel.py:133): under torch.compile with
+# max-autotune, every compatible config is benchmarked and the fastest one is compiled in.
+from torch._inductor.kernel.custom_op import register_custom_op_autotuning  # noqa: E402
 
-    register_custom_op_autotuning(
-        _autotuned_op, config_generator=lambda fake_tensors: generate_autotune_configs(fake_tensors, _CONFIGS, 1))
+register_custom_op_autotuning(
+    _autotuned_op,
+    config_generator=lambda fake_tensors: generate_autotune_configs(fake_tensors, _CONFIGS, 1,
+                                                                    decomposition=_autotune_decomposition))
+
+
+def _contiguous_inputs_first(op) -> None:
+    """Wrap the autotuning lowering of `op`: its tensor inputs reach it as contiguous, realized
+    buffers (the op needs contiguous operands anyway, and torch 2.10's autotuning cannot take an
+    unrealized view such as x.to(fp16).view(-1, K) fused into the graph), and its non-tensor
+    arguments by their schema names (torch 2.10's lowering would rename positional ones to
+    arg_<i>, which neither the op nor its decompositions accept)."""
+    from torch._inductor import ir
+    from torch._inductor.lowering import lowerings
+
+    inner = lowerings[op]
+    names = [a.name for a in op._schema.arguments]
+
+    def lowering(*args, **kwargs):
+        tensors = []
+        named = dict(kwargs)
+        for i, arg in enumerate(args):
+            if isinstance(arg, ir.TensorBox):
+                arg = ir.ExternKernel.require_contiguous(arg)
+                tensors.append(arg if isinstance(arg, ir.TensorBox) else ir.TensorBox(arg))
+            else:
+                named[names[i]] = arg
+        return inner(*tensors, **named)
+
+    lowerings[op] = lowering
+
+
+_contiguous_inputs_first(torch.ops.feather_ops_internal.scaled_mm_autotuned.default)
 
 
 def scaled_mm_hip(

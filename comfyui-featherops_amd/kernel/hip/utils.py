@@ -43,8 +43,10 @@ def _size_hint(value) -> int:
         return hint_int(value)
 
 
-def generate_autotune_configs(fake_tensors: dict, configs: list[Config], b_dim: int) -> list:
-    """Inductor config generator (utils.py:152-175)."""
+def generate_autotune_configs(fake_tensors: dict, configs: list[Config], b_dim: int,
+                              decomposition: Callable | None = None) -> list:
+    """Inductor config generator (utils.py:152-175). `decomposition`, when given, is the
+    function each config runs (else Inductor runs the op's own implementation)."""
     from torch._inductor.kernel.custom_op import CustomOpConfig
 
     a = fake_tensors["a"]
@@ -56,7 +58,8 @@ def generate_autotune_configs(fake_tensors: dict, configs: list[Config], b_dim: 
     if not compatible:
         raise RuntimeError(f"No compatible config for M={M} N={N} K={K}.")
     return [
-        CustomOpConfig(block_warps_m=c[0], block_warps_n=c[1], unroll_k=c[2], repeat_m=c[3], repeat_n=c[4])
+        CustomOpConfig(decomposition, block_warps_m=c[0], block_warps_n=c[1], unroll_k=c[2], repeat_m=c[3],
+                       repeat_n=c[4])
         for c in compatible
     ]
 

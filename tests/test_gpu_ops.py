@@ -220,3 +220,37 @@ def test_any_m_equals_padded(cuda, hk, M):
                           bias.cpu().numpy(), O.DT_F16)
     assert_gemm_close(y, ref, torch.float16, f"any-M {M}")
     assert_gemm_close(yp, ref, torch.float16, f"padded {M}")
+
+
+def test_inductor_autotunes_every_compatible_config(cuda, hk, monkeypatch):
+    """Inductor's custom-op autotuning (reference kernel/hip/hip_kernel.py:133) on this torch:
+    compiling scaled_mm_hip benchmarks the compatible configs through the op's decomposition
+    and the compiled result equals the oracle."""
+    import torch._inductor.lowering as L
+
+    assert torch.ops.feather_ops_internal.scaled_mm_autotuned.default in L.lowerings
+    seen = set()
+    real = hk._autotune_decomposition
+
+    def spy(a, b, scale, bias, **kw):
+        seen.add((kw["block_warps_m"], kw["block_warps_n"], kw["unroll_k"], kw["repeat_m"], kw["repeat_n"]))
+        return real(a, b, scale, bias, **kw)
+
+    monkeypatch.setattr(hk, "_autotune_decomposition", spy)
+    torch._dynamo.reset()
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(256, 1024, generator=g).half().to(cuda)
+    bp = hk.prepack_b_for_scaled_mm((torch.randn(1024, 768, generator=g) * 0.1).to(torch.float8_e5m2).to(cuda))
+    s = torch.tensor(1.5, device=cuda)
+    bias = (torch.randn(768, generator=g) * 0.01).bfloat16().to(cuda)
+
+    @torch.compile(fullgraph=True)
+    def f(a, bp, s, bias):
+        return hk.scaled_mm_hip(a, bp, s, bias, torch.bfloat16)
+
+    y = f(a, bp, s, bias)
+    assert len(seen) >= 2, f"autotuning ran {len(seen)} configs"
+    ref = O.scaled_mm_ref(a.cpu().numpy(), bp.view(torch.uint8).cpu().numpy(), np.float32(1.5),
+                          bias.cpu().view(torch.int16).numpy().view(np.uint16), O.DT_BF16)
+    assert_gemm_close(y, ref, torch.bfloat16, "inductor autotuned")
+    torch._dynamo.reset()
