@@ -106,11 +106,41 @@ def build_torch_ops() -> Path:
     return OPS_LIB_PATH
 
 
+def _torch_host_flags() -> tuple[list[str], list[str]]:
+    """g++ compile flags and link flags for host code against the installed torch (ROCm)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    cflags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+              f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}"]
+    cflags += [f"-I{p}" for p in cpp_extension.include_paths()] + [f"-I{rocm}/include", f"-I{INCLUDE}"]
+    # --no-as-needed: nothing references libtorch_hip directly, but loading it registers the
+    # GPU backend of the ATen ops
+    lflags = [f"-L{torch_lib}", "-Wl,--no-as-needed", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch",
+              "-Wl,--as-needed",
+              f"-Wl,-rpath,{torch_lib}", f"-L{rocm}/lib", "-lamdhip64"]
+    return cflags, lflags
+
+
+def build_libtorch_bench() -> Path:
+    """cpp_benchmarks/build/benchmark_scaled_mm_hip_libtorch: host C++ on ATen tensors, calling the C ABI."""
+    BENCH_BIN_DIR.mkdir(exist_ok=True)
+    cflags, lflags = _torch_host_flags()
+    exe = BENCH_BIN_DIR / "benchmark_scaled_mm_hip_libtorch"
+    _run([os.environ.get("CXX", "g++"), *cflags, str(BENCH_DIR / "benchmark_scaled_mm_hip_libtorch.cpp"), *lflags,
+          f"-L{LIB_DIR}", "-lfeatherops_amd", f"-Wl,-rpath,{LIB_DIR}", "-o", str(exe)])
+    return exe
+
+
 def build_benches() -> list[Path]:
     hipcc = _hipcc()
     BENCH_BIN_DIR.mkdir(exist_ok=True)
     out = []
     for src in sorted(BENCH_DIR.glob("*.cpp")):
+        if src.stem.endswith("_libtorch"):
+            continue  # host C++ against torch: build_libtorch_bench
         exe = BENCH_BIN_DIR / src.stem
         _run([hipcc, "-x", "hip", *HIP_FLAGS, str(src), f"-L{LIB_DIR}", "-lfeatherops_amd",
               f"-Wl,-rpath,{LIB_DIR}", "-o", str(exe)])
@@ -120,8 +150,8 @@ def build_benches() -> list[Path]:
 
 def build_all() -> None:
     build_library()
-    with ThreadPoolExecutor(max_workers=2) as ex:
-        jobs = [ex.submit(build_torch_ops), ex.submit(build_benches)]
+    with ThreadPoolExecutor(max_workers=3) as ex:
+        jobs = [ex.submit(build_torch_ops), ex.submit(build_benches), ex.submit(build_libtorch_bench)]
         for j in jobs:
             j.result()
 

@@ -1,0 +1,43 @@
+"""The benchmark harnesses that mirror the reference's (cpp_benchmarks/ and
+benchmark_scaled_mm_hip_configs.py) run and report: the libtorch C++ bench with its
+float64 check of the output, and the per-config sweep over every compatible tuple."""
+
+import re
+import subprocess
+import sys
+
+import pytest
+
+from conftest import REPO
+
+pytestmark = pytest.mark.gpu
+PKG = REPO / "comfyui-featherops_amd"
+
+
+def _run(cmd, cwd=REPO):
+    print("run", " ".join(map(str, cmd)), flush=True)
+    out = subprocess.run([str(c) for c in cmd], cwd=cwd, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0, out.stdout + out.stderr
+    return out.stdout
+
+
+@pytest.mark.parametrize("shape,cfg,out", [((512, 1024, 1024), (2, 4, 4, 8, 4), "fp16"),
+                                           ((48, 3072, 2048), (1, 1, 2, 1, 2), "bf16"),
+                                           ((4096, 3072, 3072), (2, 4, 4, 8, 3), "bf16")])
+def test_libtorch_bench_runs_and_checks(shape, cfg, out):
+    exe = PKG / "cpp_benchmarks" / "build" / "benchmark_scaled_mm_hip_libtorch"
+    m, n, k = shape
+    text = _run([exe, "--m", m, "--n", n, "--k", k, "--iters", 3, "--warmup", 1, "--warps_m", cfg[0], "--warps_n",
+                 cfg[1], "--unroll", cfg[2], "--repeat_m", cfg[3], "--repeat_n", cfg[4], "--out", out, "--check"])
+    assert "scaled_mm libtorch benchmark" in text and re.search(r"avg TFLOP/s: [0-9.]+", text)
+    assert "check:" in text and " ok" in text
+
+
+def test_config_sweep_script():
+    text = _run([sys.executable, "benchmark_scaled_mm_hip_configs.py", "--shapes", "256,512,512;64,1024,1024",
+                 "--rep", "3", "--warmup", "1"], cwd=PKG)
+    lines = [ln for ln in text.splitlines() if "avg_TFLOPS=" in ln]
+    assert len(lines) >= 20, text
+    assert any(ln.strip().startswith("any_m pick=") for ln in lines)
+    for ln in lines:
+        assert float(re.search(r"avg_TFLOPS=([0-9.]+)", ln).group(1)) > 0
