@@ -467,3 +467,37 @@ def test_baseline_config1_gemm(cuda, hk, quant):
     assert_gemm_close(y, ref, torch.float16, "C1 any-M")
     # the route BASELINE config 1 takes by default (split-K 64x64 tiles) is deterministic
     assert torch.equal(y, hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16))
+
+
+@pytest.mark.parametrize("M,N,K,out_dtype", [(4100, 4112, 1024, torch.float16), (2304, 9232, 512, torch.bfloat16),
+                                             (8192, 2064, 256, torch.float16)])
+def test_multi_wave_grids_ragged(cuda, M, N, K, out_dtype):
+    """Grids with more output tiles than CUs and ragged edges, through the reference ABI and
+    the workspace entry: every tile config gives the same bits (all sum K in the same order),
+    and the whole output matches a float64 evaluation and the checksums."""
+    g = torch.Generator().manual_seed(M + N)
+    packed, s = weight_like(N, K, g)
+    bias, _ = _bias_for(out_dtype, N, g)
+    gd = torch.Generator(device=cuda).manual_seed(M)
+    a = torch.randn(M, K, generator=gd, device=cuda).half()
+    bd, sd, bsd = to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), bias.to(cuda)
+    ref = torch_ref_dev(a, bd, sd, bsd, out_dtype)
+    first = None
+    L = lib()
+    for cfg in [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (2, 4, 4, 8, 3), (2, 4, 4, 4, 4), (4, 2, 4, 4, 4), (2, 2, 4, 4, 4)]:
+        print("multi-wave", M, N, K, cfg, "kernel", L.feather_scaled_mm_kernel_id(M, N, K, *cfg), flush=True)
+        y = capi_scaled_mm(a, bd, sd, bsd, out_dtype, cfg)
+        assert_gemm_close_dev(y, ref, out_dtype, f"{M}x{N}x{K} {cfg}")
+        if first is None:
+            first = y
+            assert_row_col_checksums(a, bd, sd, bsd, y, label=f"{M}x{N}x{K}")
+        else:
+            assert torch.equal(y.view(torch.int16), first.view(torch.int16)), f"{cfg} differs from the first config"
+        nbytes = L.feather_scaled_mm_workspace_size(M, N, K, *cfg)
+        ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=cuda)
+        y2 = torch.full((M, N), float("nan"), dtype=out_dtype, device=cuda)
+        assert L.feather_launch_scaled_mm_ws(a.data_ptr(), bd.data_ptr(), sd.data_ptr(), bsd.data_ptr(), y2.data_ptr(),
+                                             M, N, K, 1, 1, *cfg, 1, 0 if out_dtype == torch.float16 else 1,
+                                             ws.data_ptr(), nbytes, stream(cuda))
+        torch.cuda.synchronize()
+        assert torch.equal(y2.view(torch.int16), first.view(torch.int16)), f"{cfg} workspace entry differs"
