@@ -15,6 +15,9 @@
 // --quant: time feather_quantize_prepack_e5m2 on an N x K fp16 weight instead
 // (amax pass + quantize/prepack pass, 5 bytes per element of algorithmic
 // traffic: 2 read for the amax, 2 read + 1 written for the codes).
+// --lora-down R: time feather_lora_down instead, T (M x R) = x (M x K) . D^T
+// with bf16 x ~ U[-1, 1) rotated over --rotate buffers and D (R x K), GB/s on
+// the bytes of x, D and T.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -51,12 +54,14 @@ struct Opts {
     int b_dtype = FEATHER_B_E5M2;
     int rotate = 1;
     bool quant = false;
+    int64_t lora_rank = 0;
 };
 
 void usage(const char* argv0) {
     std::cout << "Usage: " << argv0
               << " [--m M] [--n N] [--k K] [--warmup W] [--iters I] [--warps_m M] [--warps_n N] [--unroll U]"
-                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant]\n";
+                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant]"
+                 " [--lora-down R]\n";
 }
 
 Opts parse(int argc, char** argv) {
@@ -84,6 +89,7 @@ Opts parse(int argc, char** argv) {
         else if (a == "--b") o.b_dtype = val() == "e4m3" ? FEATHER_B_E4M3FN : FEATHER_B_E5M2;
         else if (a == "--rotate") o.rotate = std::max(1, std::stoi(val()));
         else if (a == "--quant") o.quant = true;
+        else if (a == "--lora-down") o.lora_rank = std::stoll(val());
         else if (a == "--help" || a == "-h") {
             usage(argv[0]);
             std::exit(0);
@@ -162,11 +168,77 @@ int run_quant(const Opts& o) {
     return 0;
 }
 
+uint16_t to_bf16_bits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// T = x . D^T through feather_lora_down (bf16), x rotated over o.rotate buffers.
+int run_lora_down(const Opts& o) {
+    const int64_t M = o.m, K = o.k, R = o.lora_rank;
+    const size_t nx = static_cast<size_t>(M) * K, nd = static_cast<size_t>(R) * K, nt = static_cast<size_t>(M) * R;
+    std::mt19937 gen(42);
+    std::uniform_real_distribution<float> uni(-1.f, 1.f);
+    std::vector<uint16_t> hx(nx), hd(nd);
+    for (auto& v : hx) v = to_bf16_bits(uni(gen));
+    for (auto& v : hd) v = to_bf16_bits(0.05f * uni(gen));
+    std::vector<void*> dx(o.rotate);
+    for (auto& p : dx) {
+        HIP_OK(hipMalloc(&p, nx * 2));
+        HIP_OK(hipMemcpy(p, hx.data(), nx * 2, hipMemcpyHostToDevice));
+    }
+    void *dd, *dt, *dws = nullptr;
+    HIP_OK(hipMalloc(&dd, nd * 2));
+    HIP_OK(hipMalloc(&dt, nt * 2));
+    HIP_OK(hipMemcpy(dd, hd.data(), nd * 2, hipMemcpyHostToDevice));
+    const size_t ws = feather_lora_down_workspace_size(M, K, R);
+    if (ws) {
+        HIP_OK(hipMalloc(&dws, ws));
+        HIP_OK(hipMemset(dws, 0, ws));
+    }
+    hipStream_t stream;
+    hipEvent_t t0, t1;
+    HIP_OK(hipStreamCreate(&stream));
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+    auto run = [&](int i) {
+        const int rc = feather_lora_down(dx[i % o.rotate], FEATHER_DTYPE_BF16, dd, dt, M, K, R, dws, ws, stream);
+        if (rc != FEATHER_OK) {
+            std::cerr << "lora_down failed: " << feather_status_string(rc) << std::endl;
+            std::exit(1);
+        }
+    };
+    for (int i = 0; i < o.warmup; ++i) run(i);
+    HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipEventRecord(t0, stream));
+    for (int i = 0; i < o.iters; ++i) run(i);
+    HIP_OK(hipEventRecord(t1, stream));
+    HIP_OK(hipEventSynchronize(t1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+    ms /= o.iters;
+    const double bytes = 2.0 * (nx + nd + nt);
+    std::cout << std::fixed << std::setprecision(4);
+    std::cout << "lora_down benchmark\n  problem: m=" << M << " k=" << K << " rank=" << R << " bf16 rotate=" << o.rotate
+              << " workspace=" << ws << "\n  back-to-back ms: " << ms << "  (GB/s " << bytes / ms / 1e6
+              << " on x + D + T)" << std::endl;
+    for (auto p : dx) HIP_OK(hipFree(p));
+    HIP_OK(hipFree(dd));
+    HIP_OK(hipFree(dt));
+    if (dws) HIP_OK(hipFree(dws));
+    HIP_OK(hipEventDestroy(t0));
+    HIP_OK(hipEventDestroy(t1));
+    HIP_OK(hipStreamDestroy(stream));
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     const Opts o = parse(argc, argv);
     if (o.quant) return run_quant(o);
+    if (o.lora_rank > 0) return run_lora_down(o);
     if (o.k % (16 * o.u) != 0) {
         std::cerr << "K must be divisible by 16 * unroll_k (" << 16 * o.u << ")" << std::endl;
         return 1;
