@@ -100,3 +100,34 @@ def test_noalloc_rejects_a_split_larger_than_the_array():
     assert out.returncode == 0, out.stderr
     need, st, msg = out.stdout.split(maxsplit=2)
     assert int(need) > 16 << 20 and int(st) == FEATHER_ERR_SCRATCH and "scratch" in msg
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(cuda):
+    """The entry's use case: calls captured in a HIP graph (no allocation during capture) and
+    replayed, with eager work between replays; every replay equals the eager workspace entry."""
+    shapes = [(16, 5120, 13824, (1, 1, 2, 1, 2)), (64, 4096, 4096, (2, 2, 4, 4, 4))]
+    ops = []
+    for i, (M, N, K, cfg) in enumerate(shapes):
+        a, bd, sd, bias = _operands(M, N, K, 300 + i, cuda)
+        ref, _ = _run_ex(a, bd, sd, bias, M, N, K, cfg, 0)
+        _run_noalloc(a, bd, sd, bias, M, N, K, cfg, 0)  # set-up call (symbol address) before capture
+        out = torch.empty(M, N, dtype=torch.float16, device=cuda)
+        ops.append((a, bd, sd, bias, out, ref, M, N, K, cfg))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        s = torch.cuda.current_stream().cuda_stream
+        for a, bd, sd, bias, out, _, M, N, K, cfg in ops:
+            st = lib().feather_launch_scaled_mm_noalloc(a.data_ptr(), 0, bd.data_ptr(), sd.data_ptr(), bias.data_ptr(),
+                                                        out.data_ptr(), M, N, K, 1, 1, *cfg, 1, 0, s)
+            assert st == FEATHER_OK
+    for rep in range(4):
+        for op in ops:
+            op[4].zero_()
+        graph.replay()
+        junk = torch.randn(1 << 16, device=cuda).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        for op in ops:
+            assert torch.equal(op[4].view(torch.int16), op[5].view(torch.int16)), f"replay {rep} {op[6:9]}"
+        assert torch.isfinite(junk)
