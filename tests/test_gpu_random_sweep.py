@@ -115,3 +115,27 @@ def test_random_any_m_lora(cuda, hk, seed):
             yr = base.to(out) + torch.mm(t, u.t()).to(out)
             ref = yr.numpy() if out == torch.float16 else yr.view(torch.int16).numpy().view(np.uint16)
         assert_gemm_close(y, ref, out, label)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_lora_down(cuda, hk, seed):
+    """The LoRA down-projection over random row counts, K and ranks (K split across workgroups
+    or not, rank chunks of 128 plus a remainder), both dtypes, back to back on one stream
+    through the torch op (one shared workspace), against the oracle's lora_down_ref."""
+    rng = np.random.default_rng(200 + seed)
+    for case in range(24):
+        M = int(rng.choice([1, 5, 64, 65, 300, 1000, 2048, 4100, 9000]))
+        K = 8 * int(rng.integers(1, 700))
+        R = 32 * int(rng.integers(1, 9))
+        dt = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        g = torch.Generator().manual_seed(5000 * seed + case)
+        x = torch.randn(M, K, generator=g).to(dt)
+        d = (torch.randn(R, K, generator=g) * 0.05).to(dt)
+        t = torch.ops.feather_ops.lora_down.default(x.to(cuda), d.to(cuda))
+        torch.cuda.synchronize()
+        if dt == torch.float16:
+            ref = O.lora_down_ref(x.numpy(), d.numpy(), O.DT_F16)
+        else:
+            ref = O.lora_down_ref(x.view(torch.int16).numpy().view(np.uint16),
+                                  d.view(torch.int16).numpy().view(np.uint16), O.DT_BF16)
+        assert_gemm_close(t, ref, dt, f"seed {seed} case {case}: M={M} K={K} R={R} {dt}")
