@@ -9,10 +9,14 @@ per-tensor scale and bias, inputs resident in HBM. The weight is a synthetic
 quantize kernel; A ~ N(0, 1).
 
 Also measured in the same run (extra keys of the JSON line):
+  bf16_activations  the headline shape with bf16 activations through the
+              any-M op, beside fp16 activations and torch's cast + the GEMM
   small_m     config 2 (M=16, K=N=4096): GB/s, rotating over enough distinct
               weights (> 256 MB) that the Infinity Cache cannot serve them
   quantize    quantize+prepack of a 13824x5120 fp16 weight (config 5's op),
               four weights in rotation so they stream from HBM
+  lora        an unmerged rank-64 LoRA layer on the headline shape, fused
+              epilogue against the reference's separate pass
   configs     every BASELINE config at one GPU: C1 (M=256, K=N=1024), C3
               (image-DiT linears, M=4096, bf16 out), C4 (video-DiT linears,
               M=32768), C5 (40-block x 6-linear stack at M=32768: on-device
@@ -455,6 +459,24 @@ def main() -> int:
                                                     "TFLOP_per_s": round(flops / (ms_ref * 1e-3) / 1e12, 2)}
         log(f"bench: torch fp16 matmul (hipBLASLt) same shape {ms_ref:.3f} ms")
         del b16
+
+        # bf16 activations on the headline shape through the any-M op (the
+        # large tiles round them to fp16 with the library's RNE cast pass, then
+        # run the fp16 GEMM), beside the reference's route: x.to(float16)
+        # (comfy_feather/ops.py:88) followed by the same GEMM
+        abf = a.to(torch.bfloat16)
+        any_m = torch.ops.feather_ops.scaled_mm_any_m.default
+        for _ in range(2):
+            any_m(abf, bp, scale, bias, torch.float16)
+        ms_bf = time_launches(lambda _i: any_m(abf, bp, scale, bias, torch.float16), max(3, args.steps // 2))
+        ms_f16 = time_launches(lambda _i: any_m(a, bp, scale, bias, torch.float16), max(3, args.steps // 2))
+        ms_refroute = time_launches(lambda _i: any_m(abf.to(torch.float16), bp, scale, bias, torch.float16),
+                                    max(3, args.steps // 2))
+        result["bf16_activations"] = {"ms": round(ms_bf, 4), "fp16_activations_ms": round(ms_f16, 4),
+                                      "torch_cast_then_gemm_ms": round(ms_refroute, 4),
+                                      "route": "library RNE cast pass + fp16 GEMM (any-M op)"}
+        log(f"bench: bf16 activations {ms_bf:.3f} ms (fp16 {ms_f16:.3f}, torch cast + GEMM {ms_refroute:.3f})")
+        del abf
     del a, c
 
     if not args.only_headline:
