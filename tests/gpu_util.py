@@ -50,7 +50,7 @@ def _ulp(x: np.ndarray, mant_bits: int) -> np.ndarray:
     return 2.0 ** (np.floor(np.log2(ax)) - mant_bits)
 
 
-def assert_gemm_close(out, ref, out_dtype, label=""):
+def assert_gemm_close(out, ref, out_dtype, label="", literal=False):
     """Parity gate against the oracle (both rounded to the output type).
 
     rel-Frobenius <= 1e-3 and every element within max(2e-2, 2 ulp of the
@@ -62,7 +62,10 @@ def assert_gemm_close(out, ref, out_dtype, label=""):
     fp16 above |y| = 20.48, one ulp exceeds 2e-2). Seen with the split-K tiles:
     acc*s = 83.71875095 (a hair above the fp16 tie 83.71875) rounds up in
     float64 and down in a reassociated fp32 sum; + bias 0.375 then lands on
-    84.125 vs 84.0. Non-finite values must agree exactly."""
+    84.125 vs 84.0. Non-finite values must agree exactly. With literal=True the
+    north-star gate is also applied as written (max-abs <= 2e-2, no ulp
+    allowance): it holds for fp16 outputs at the BASELINE data scales, where
+    |y| stays far below 20.48."""
     o = out_to_f32(out)
     r = out_to_f32(ref)
     fin = np.isfinite(r)
@@ -75,6 +78,8 @@ def assert_gemm_close(out, ref, out_dtype, label=""):
     worst = float((d / tol).max()) if d.size else 0.0
     assert fro <= 1e-3, f"{label}: rel-Fro {fro:.3g} > 1e-3"
     assert worst <= 1.0, f"{label}: max |diff|/tol = {worst:.3g} (max abs {d.max():.3g})"
+    if literal and d.size:
+        assert float(d.max()) <= 2e-2, f"{label}: max abs {d.max():.3g} > 2e-2"
     return float(d.max()) if d.size else 0.0, float(fro)
 
 
@@ -110,8 +115,9 @@ def torch_ref_dev(a, bp, scale, bias, out_dtype, b_dtype=torch.float8_e5m2):
     return y
 
 
-def assert_gemm_close_dev(out, ref, out_dtype, label=""):
-    """assert_gemm_close's gate evaluated on the device over the whole output (same bounds)."""
+def assert_gemm_close_dev(out, ref, out_dtype, label="", literal=False):
+    """assert_gemm_close's gate evaluated on the device over the whole output (same bounds,
+    same literal option)."""
     o = out.double()
     r = ref.double()
     assert torch.equal(torch.isnan(o), torch.isnan(r)), f"{label}: NaN pattern differs"
@@ -132,6 +138,9 @@ def assert_gemm_close_dev(out, ref, out_dtype, label=""):
         flat = fin.nonzero()[i].tolist()
         raise AssertionError(f"{label}: max |diff|/tol = {worst:.3g} at {flat}: got {o[i].item()!r}, "
                              f"want {r[i].item()!r}")
+    if literal and d.numel():
+        dmax = d.max().item()
+        assert dmax <= 2e-2, f"{label}: max abs {dmax:.3g} > 2e-2"
     return fro
 
 
