@@ -214,6 +214,25 @@ def test_bf16_to_fp16_rne_exhaustive(cuda, pkg):
     assert torch.equal(out, xr.to(torch.float16))
 
 
+def test_bf16_to_fp16_large_streaming_path(cuda):
+    """Inputs of 64 Mi elements and more take the cast's nontemporal-access variant: RNE equals
+    torch's cast, RTZ equals the same data cast in pieces below that size (the ordinary
+    variant, itself pinned exhaustively above); the element count is odd (tail path)."""
+    n = (64 << 20) + 7
+    x = torch.randn(n, dtype=torch.bfloat16, device=cuda) * 3000
+    out = torch.empty(n, dtype=torch.float16, device=cuda)
+    assert lib().feather_bf16_to_fp16_rne(x.data_ptr(), out.data_ptr(), n, stream(cuda)) == 0
+    assert torch.equal(out, x.to(torch.float16))
+    assert lib().feather_bf16_to_fp16(x.data_ptr(), out.data_ptr(), n, stream(cuda)) == 0
+    pieces = torch.empty_like(out)
+    step = 1 << 24
+    for o in range(0, n, step):
+        m = min(step, n - o)
+        assert lib().feather_bf16_to_fp16(x[o:].data_ptr(), pieces[o:].data_ptr(), m, stream(cuda)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), pieces.view(torch.int16))
+
+
 def test_config5_weight_on_device(cuda, quant):
     """Config 5 quantizes 5120x13824 weights on the device: sampled rows vs the oracle."""
     gd = torch.Generator(device=cuda).manual_seed(5)
