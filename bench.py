@@ -195,7 +195,7 @@ def cpu_baseline(budget_s: float = 12.0):
                                           "to fp16 (the oracle's numpy formulation); weight decoded once, untimed"}}
 
 
-CANDIDATE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (2, 4, 4, 8, 3), (2, 2, 4, 4, 4)]
+CANDIDATE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (2, 4, 4, 8, 3), (2, 4, 4, 4, 6), (2, 2, 4, 4, 4)]
 
 
 def _gemm_shape(dev, op, quant, g, M, N, K, out_dtype, seed, reps=10):

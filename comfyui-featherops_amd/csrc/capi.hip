@@ -20,14 +20,14 @@ struct Cfg {
 };
 
 // Reference configurations (kernel/hip/hip_kernel.py:60-89, hip_kernel.cu:603-630)
-// followed by four gfx950 tiles the reference has no tuple for.
+// followed by five gfx950 tiles the reference has no tuple for.
 constexpr Cfg kConfigs[] = {
     {1, 1, 2, 1, 2}, {1, 1, 4, 1, 2}, {1, 2, 2, 1, 2}, {1, 2, 4, 1, 2}, {1, 4, 2, 1, 2}, {1, 4, 4, 1, 2},
     {1, 8, 2, 1, 2}, {1, 8, 4, 1, 2}, {1, 1, 2, 2, 2}, {1, 1, 4, 2, 2}, {1, 1, 2, 4, 4}, {1, 1, 4, 4, 4},
     {1, 2, 2, 2, 2}, {1, 2, 4, 2, 2}, {2, 1, 2, 2, 2}, {2, 1, 4, 2, 2}, {1, 4, 2, 4, 2}, {1, 4, 4, 4, 2},
     {1, 8, 2, 8, 2}, {1, 8, 4, 8, 2}, {2, 2, 2, 4, 4}, {2, 2, 4, 4, 4}, {2, 4, 2, 4, 2}, {2, 4, 4, 4, 2},
     {2, 4, 2, 4, 4}, {2, 4, 4, 4, 4}, {4, 2, 2, 2, 4}, {4, 2, 4, 2, 4},
-    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4}, {4, 2, 4, 4, 8}, {2, 4, 4, 8, 3},
+    {2, 4, 4, 8, 4}, {4, 2, 4, 4, 4}, {4, 2, 4, 4, 8}, {2, 4, 4, 8, 3}, {2, 4, 4, 4, 6},
 };
 
 bool known_config(int wm, int wn, int u, int rm, int rn) {
@@ -46,6 +46,7 @@ int tile_kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     const int bn = 16 * wn * rn;
     const bool lds = K % 64 == 0;
     if (bm >= 256 && bn == 192) return lds ? feather::kLds256x192 : feather::kTile256x128;
+    if (bm == 128 && bn == 384) return lds ? feather::kLds128x384 : feather::kTile128x128;
     if (bm >= 256 && bn >= 256) {
         if (!lds) return feather::kTile256x256;
         return wm > wn ? feather::kLds256x256w4x2 : feather::kLds256x256w2x4;
@@ -463,7 +464,7 @@ int feather_scaled_mm_pick_config(int64_t M, int64_t N, int64_t K, int* cfg) {
     };
     static const Cand cands[] = {
         {{2, 4, 4, 8, 4}, 256, 256, 1.00}, {{2, 4, 4, 8, 3}, 256, 192, 0.85}, {{2, 4, 4, 4, 4}, 128, 256, 0.90},
-        {{4, 2, 4, 4, 4}, 256, 128, 0.84}, {{2, 2, 4, 4, 4}, 128, 128, 0.80},
+        {{4, 2, 4, 4, 4}, 256, 128, 0.84}, {{2, 2, 4, 4, 4}, 128, 128, 0.80}, {{2, 4, 4, 4, 6}, 128, 384, 0.87},
     };
     Cfg best = {1, 1, 2, 1, 2};  // M <= 64: the small-M kernel
     if (M > 64) {

@@ -45,6 +45,7 @@ enum KernelId : int {
     kLds128x256 = 23,
     kLds128x128 = 24,
     kLds256x192 = 25,
+    kLds128x384 = 26,
     // LDS-DMA tiles with a K split across workgroups (small shapes)
     kLdsSk64x64 = 30,
     kLdsSk32x128 = 34,

@@ -543,7 +543,8 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
     if (p.lora_dtype != 0) {
         // rank-R epilogue: the default schedule's large tiles, fp16 activations,
         // e5m2 weights, no K split
-        if constexpr (PIPE == 1 && BM >= 128) {
+        // (the T and U chunks must fit a stage buffer: not the 128 x 384 tile)
+        if constexpr (PIPE == 1 && BM >= 128 && BM * 128 + BN * 64 >= (BM > BN ? BM : BN) * 128) {
             if (p.a_bf16 || p.b_e4m3 || ksplit != 1) return false;
             if (p.lora_dtype == 1) {
                 if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, false, 1);
@@ -592,6 +593,7 @@ bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks 
         case kLds128x256: return launch_lds<128, 256, 2, 4, PIPE>(p, stream);
         case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
         case kLds256x192: return launch_lds<256, 192, 2, 4, PIPE>(p, stream);
+        case kLds128x384: return launch_lds<128, 384, 2, 4, PIPE>(p, stream);
         case kLdsSk64x64: return launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters);
         case kLdsSk32x128: return launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
         default: return false;

@@ -259,8 +259,15 @@ at::Tensor scaled_mm_any_m_lora(const at::Tensor& a, const at::Tensor& b_prepack
     const int status = feather_scaled_mm_pick_config(M, N, K, cfg);
     TORCH_CHECK(status == FEATHER_OK, "feather_scaled_mm_pick_config failed: ", feather_status_string(status));
     const int b_dtype = b_prepacked.scalar_type() == at::kFloat8_e4m3fn ? 0 : 1;
-    const int kid = feather_scaled_mm_kernel_id(M, N, K, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]);
-    // the fused epilogue: large LDS tiles (kernel ids 20-29), e5m2 weights
+    int kid = feather_scaled_mm_kernel_id(M, N, K, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]);
+    if (kid == 26) {
+        // the 128 x 384 tile's stage buffers cannot hold 64 ranks of its U rows, so it has no rank-R
+        // epilogue: the 256 x 192 tile covers the same grids (256 tiles at M = 4096, N = 3072)
+        const int alt[5] = {2, 4, 4, 8, 3};
+        for (int i = 0; i < 5; ++i) cfg[i] = alt[i];
+        kid = feather_scaled_mm_kernel_id(M, N, K, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4]);
+    }
+    // the fused epilogue: large LDS tiles (kernel ids 20-29 but 26), e5m2 weights
     if (kid >= 20 && kid < 30 && b_dtype == 1) {
         at::Tensor c = at::empty({M, N}, a.options().dtype(out_dtype));
         check_args(a, b_prepacked, scale, bias, c, cfg[0], cfg[1], cfg[2], cfg[3], cfg[4], b_dtype, false, true);

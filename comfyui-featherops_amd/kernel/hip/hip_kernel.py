@@ -162,17 +162,17 @@ def kernel_id(M: int, N: int, K: int, cfg) -> int:
 _configured_op = torch.ops.feather_ops_internal.scaled_mm_configured.default
 scaled_mm_hip_configured = _configured_op
 
-# Reference configurations (hip_kernel.py:60-89), then four gfx950 tiles:
+# Reference configurations (hip_kernel.py:60-89), then five gfx950 tiles:
 # (2,4,4,8,4) -> 256x256 (2x4 waves), (4,2,4,4,8) -> 256x256 (4x2 waves),
-# (4,2,4,4,4) -> 256x128 and (2,4,4,8,3) -> 256x192 output tiles (the last one
-# gives M=4096, N=3072 exactly 256 tiles, one per CU).
+# (4,2,4,4,4) -> 256x128, (2,4,4,8,3) -> 256x192 and (2,4,4,4,6) -> 128x384
+# output tiles (the last two give M=4096, N=3072 exactly 256 tiles, one per CU).
 _CONFIGS = [
     (1, 1, 2, 1, 2), (1, 1, 4, 1, 2), (1, 2, 2, 1, 2), (1, 2, 4, 1, 2), (1, 4, 2, 1, 2), (1, 4, 4, 1, 2),
     (1, 8, 2, 1, 2), (1, 8, 4, 1, 2), (1, 1, 2, 2, 2), (1, 1, 4, 2, 2), (1, 1, 2, 4, 4), (1, 1, 4, 4, 4),
     (1, 2, 2, 2, 2), (1, 2, 4, 2, 2), (2, 1, 2, 2, 2), (2, 1, 4, 2, 2), (1, 4, 2, 4, 2), (1, 4, 4, 4, 2),
     (1, 8, 2, 8, 2), (1, 8, 4, 8, 2), (2, 2, 2, 4, 4), (2, 2, 4, 4, 4), (2, 4, 2, 4, 2), (2, 4, 4, 4, 2),
     (2, 4, 2, 4, 4), (2, 4, 4, 4, 4), (4, 2, 2, 2, 4), (4, 2, 4, 2, 4),
-    (2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3),
+    (2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3), (2, 4, 4, 4, 6),
 ]
 _CONFIGS = sorted(_CONFIGS, key=lambda x: (x[0], x[1], x[3], x[4], x[2]))
 

@@ -119,6 +119,31 @@ def test_fused_route_is_taken_and_deterministic(cuda, hk, pkg):
                                                *hk.any_m_config(16, N, K), 1, 1, 0)
 
 
+def test_fused_route_when_the_pick_has_no_lora_epilogue(cuda, hk, pkg):
+    """At M=4096, N=3072 the any-M pick is the 128x384 tile, which has no rank-R epilogue: the C ABI
+    refuses it, and the LoRA op runs the fused epilogue on the 256x192 tile (same 256-tile grid)."""
+    from featherops_amd.comfy_feather import lora
+
+    M, N, K = 4096, 3072, 512
+    assert hk.any_m_config(M, N, K) == (2, 4, 4, 4, 6)
+    x, bp, s, bias, wf, expect = _setup(cuda, hk, M, N, K, 11, torch.bfloat16, torch.bfloat16, ranks=(32,))
+    t, u = lora.lora_factors(x, wf)
+    x16 = x.to(torch.float16)
+    c = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    L = hk._lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    args = (x16.data_ptr(), bp.data_ptr(), s.data_ptr(), bias.data_ptr(), c.data_ptr(), M, N, K, 1, 1, t.data_ptr(),
+            u.data_ptr(), t.shape[1], 1)
+    assert not L.feather_launch_scaled_mm_lora(*args, 2, 4, 4, 4, 6, 1, 1, st)
+    assert L.feather_launch_scaled_mm_lora(*args, 2, 4, 4, 8, 3, 1, 1, st)
+    y = hk.scaled_mm_hip_any_m_lora(x, bp, s, bias, torch.bfloat16, t, u)
+    torch.cuda.synchronize()
+    assert torch.equal(c, y)
+    rows = torch.tensor([0, 1, 255, 256, 2047, 4095], device=cuda)
+    ref = _fused_ref(x[rows], bp, s, bias, torch.bfloat16, t[rows], u)
+    assert_gemm_close(y[rows], ref, torch.bfloat16, "4096x3072 fused LoRA")
+
+
 def test_any_m_lora_argument_checks(cuda, hk, pkg):
     M, N, K = 256, 512, 256
     x = torch.zeros(M, K, dtype=torch.float16, device=cuda)

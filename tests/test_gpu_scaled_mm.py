@@ -12,7 +12,7 @@ from oracle import feather_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-TILE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3), (2, 4, 4, 4, 4), (4, 2, 4, 2, 4), (1, 8, 4, 8, 2), (1, 1, 2, 2, 2)]
+TILE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3), (2, 4, 4, 4, 6), (2, 4, 4, 4, 4), (4, 2, 4, 2, 4), (1, 8, 4, 8, 2), (1, 1, 2, 2, 2)]
 
 
 def _bias_for(out_dtype, n, gen):

@@ -63,16 +63,18 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(4096, 4096, 4096, (3, 3, 3, 3, 3)) == 0
     assert hk.kernel_id(4096, 4096, 4090, (2, 4, 4, 8, 4)) == 0  # K % 16 != 0
     assert hk.kernel_id(4096, 3072, 3072, (2, 4, 4, 8, 3)) == 25  # 256x192
+    assert hk.kernel_id(4096, 3072, 3072, (2, 4, 4, 4, 6)) == 26  # 128x384
+    assert hk.kernel_id(4096, 3072, 3088, (2, 4, 4, 4, 6)) == 4  # K % 64 != 0: register-staged 128x128
     assert hk.kernel_id(4096, 3072, 3080, (2, 4, 4, 8, 3)) == 0  # K % 16 != 0
     for cfg in hk._CONFIGS:
-        assert hk.kernel_id(4096, 4096, 4096, cfg) in (5, 6, 20, 21, 22, 23, 24, 25)
+        assert hk.kernel_id(4096, 4096, 4096, cfg) in (5, 6, 20, 21, 22, 23, 24, 25, 26)
         assert hk.kernel_id(1024, 1024, 1024, cfg) == 30
 
 
 def test_pick_config(hk):
     """The any-M entry's shape-based tile pick (256 CUs assumed without a GPU)."""
     assert hk.any_m_config(32768, 13824, 5120) == (2, 4, 4, 8, 4)  # 256x256, 27 full waves
-    assert hk.any_m_config(4096, 3072, 3072) == (2, 4, 4, 8, 3)  # 256x192: 256 tiles, one per CU
+    assert hk.any_m_config(4096, 3072, 3072) == (2, 4, 4, 4, 6)  # 128x384: 256 tiles, one per CU
     assert hk.any_m_config(512, 9216, 3072) == (2, 4, 4, 4, 4)  # 128x256: 144 tiles in one wave
     assert hk.any_m_config(16, 4096, 4096) == (1, 1, 2, 1, 2)  # small-M kernel
     for shape in [(100, 3072, 3072), (1000, 5120, 13824), (65, 768, 512)]:
