@@ -27,6 +27,11 @@ Also measured in the same run (extra keys of the JSON line):
               CPU matmul) on up to 16 host cores, on a bounded sample of the
               headline rows
 
+The headline is W untimed warmup steps, then K timed steps between HIP events.
+Every extra key runs ~25 ms untimed before ~25 ms of timed calls
+(time_steady): its kernels are short against the tens of ms the engine clock
+takes to rise under load.
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
 """
 
