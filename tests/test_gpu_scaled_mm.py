@@ -486,7 +486,8 @@ def test_multi_wave_grids_ragged(cuda, M, N, K, out_dtype):
     ref = torch_ref_dev(a, bd, sd, bsd, out_dtype)
     first = None
     L = lib()
-    for cfg in [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (2, 4, 4, 8, 3), (2, 4, 4, 4, 4), (4, 2, 4, 4, 4), (2, 2, 4, 4, 4)]:
+    for cfg in [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (2, 4, 4, 8, 3), (2, 4, 4, 4, 6), (2, 4, 4, 4, 4), (4, 2, 4, 4, 4),
+                (2, 2, 4, 4, 4)]:
         print("multi-wave", M, N, K, cfg, "kernel", L.feather_scaled_mm_kernel_id(M, N, K, *cfg), flush=True)
         y = capi_scaled_mm(a, bd, sd, bsd, out_dtype, cfg)
         assert_gemm_close_dev(y, ref, out_dtype, f"{M}x{N}x{K} {cfg}")
