@@ -158,6 +158,37 @@ def test_inf_nan_propagation(cuda):
         assert torch.isinf(y).all()
 
 
+@pytest.mark.parametrize("splitk", ["0", ""])
+@pytest.mark.parametrize("cfg", [(2, 4, 4, 8, 4), (2, 4, 4, 4, 6), (2, 4, 4, 8, 3), (1, 1, 2, 1, 2)])
+def test_bf16_output_nan_is_canonical(cuda, monkeypatch, cfg, splitk):
+    """bf16 outputs: NaN results carry torch's canonical 0x7fc0 (its float -> bfloat16 cast), from a
+    NaN activation, from inf - inf in the sum and from a NaN bias; every other element matches the
+    oracle; rows without non-finite inputs are unaffected (the epilogue redoes a wave's conversion
+    only when that wave produced a NaN)."""
+    M, K, N = 256, 128, 384
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(M, K, generator=g).half()
+    a[3, 5] = float("nan")
+    a[70, 9] = float("inf")
+    a[70, 10] = float("inf")
+    codes = np.full((K, N), 0x3C, np.uint8)
+    codes[9, 200] = 0xBC  # +inf * -1 meets +inf * +1 in column 200 of row 70: NaN (+inf elsewhere)
+    packed = O.prepack_kn(codes)
+    bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    bias[17] = float("nan")
+    bias_np = bias.view(torch.int16).numpy().view(np.uint16)
+    ref = O.scaled_mm_ref(a.numpy(), packed, None, bias_np, O.DT_BF16)
+    if splitk:  # the tuple's own tile instead of the split-K route this size takes by default
+        monkeypatch.setenv("FEATHEROPS_SPLITK", splitk)
+    y = capi_scaled_mm(a.to(cuda), to_dev_codes(packed, cuda), None, bias.to(cuda), torch.bfloat16, cfg)
+    bits = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    nan = (ref & 0x7FFF) > 0x7F80
+    assert nan[3].all() and nan[:, 17].all() and nan[70, 200]
+    assert np.array_equal((bits & 0x7FFF) > 0x7F80, nan), cfg
+    assert (bits[nan] == 0x7FC0).all(), sorted(set(bits[nan].tolist()))[:8]
+    assert_gemm_close(y, ref, torch.bfloat16, f"bf16 nan {cfg}")
+
+
 def test_deterministic(cuda):
     g = torch.Generator().manual_seed(9)
     a = torch.randn(512, 1024, generator=g).half().to(cuda)
