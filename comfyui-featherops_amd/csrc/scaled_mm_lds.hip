@@ -554,12 +554,14 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
     const int group_m = p.group_m > 0 ? p.group_m : 4;
-    // Outputs of 64 MB and more are written with nontemporal stores: they are
-    // never re-read here, and a one-wave grid then has less dirty data to
-    // write back at its end (measured on MI355X: M=32768 N=13824 K=5120
-    // 3.096 -> 3.081 ms, M=32768 N=K=5120 1.145 -> 1.139 ms). Smaller outputs
-    // keep ordinary stores, so they can stay in the MALL for the next layer.
-    const int c_nt = p.M * p.N * 2 >= (int64_t(64) << 20) ? 1 : 0;
+    // Outputs larger than the 256 MB MALL are written with nontemporal stores:
+    // they are never re-read here and cannot stay cached for the next layer
+    // anyway (M=32768 N=13824 K=5120 3.096 -> 3.081 ms on MI355X). Smaller
+    // outputs keep ordinary stores: nontemporal ones measured ~2% faster for an
+    // isolated one-wave M=4096 N=3072 GEMM, but a chained FFN (M=4096,
+    // 3072 -> 12288 -> 3072) took 414 us with ordinary stores and 419 us with
+    // the 100 MB intermediate written nontemporally.
+    const int c_nt = p.M * p.N * 2 > (int64_t(256) << 20) ? 1 : 0;
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
 #define FEATHER_LDS_LAUNCH_L(BF, E4, AB, LORA)                                                                        \
