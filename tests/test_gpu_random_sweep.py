@@ -139,3 +139,39 @@ def test_random_lora_down(cuda, hk, seed):
             ref = O.lora_down_ref(x.view(torch.int16).numpy().view(np.uint16),
                                   d.view(torch.int16).numpy().view(np.uint16), O.DT_BF16)
         assert_gemm_close(t, ref, dt, f"seed {seed} case {case}: M={M} K={K} R={R} {dt}")
+
+
+def test_random_large_shapes(cuda, hk):
+    """Seeded shapes of the size the large tiles serve (M 1000-6000, N often a multiple of 384 so the
+    128x384 pick appears, ragged M and N), fp16 and bf16 outputs, bias on or off, an occasional NaN
+    activation or bias entry: the any-M op over the whole output against a float64 evaluation on
+    the device, canonical bf16 NaNs, and the 128x384 tile through the C ABI where its blocks divide."""
+    from gpu_util import assert_gemm_close_dev, capi_scaled_mm, torch_ref_dev
+
+    rng = np.random.default_rng(42)
+    gd = torch.Generator(device=cuda).manual_seed(42)
+    for case in range(12):
+        M = int(rng.integers(1000, 6000))
+        N = 384 * int(rng.integers(1, 12)) if rng.random() < 0.5 else 16 * int(rng.integers(20, 700))
+        K = 64 * int(rng.integers(1, 60)) if rng.random() < 0.8 else 16 * int(rng.integers(10, 300))
+        out = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+        has_b = rng.random() < 0.7
+        a = torch.randn(M, K, generator=gd, device=cuda).half()
+        w = torch.randn(N, K, generator=gd, device=cuda) * 0.02
+        s = (w.abs().max() / 57344.0).float().reshape(1)
+        bp = (w / s).to(torch.float8_e5m2).view(N, K // 16, 16).permute(1, 0, 2).contiguous()
+        bias = (torch.randn(N, generator=gd, device=cuda) * 0.1).to(out) if has_b else None
+        if rng.random() < 0.3:
+            a[int(rng.integers(0, M)), int(rng.integers(0, K))] = float("nan")
+        if has_b and rng.random() < 0.3:
+            bias[int(rng.integers(0, N))] = float("nan")
+        cfg = hk.any_m_config(M, N, K)
+        print("large", case, M, N, K, out, has_b, cfg, flush=True)
+        ref = torch_ref_dev(a, bp, s, bias, out)
+        y = hk.scaled_mm_hip_any_m(a, bp, s, bias, out)
+        assert_gemm_close_dev(y, ref, out, f"large {case} {cfg}")
+        if out == torch.bfloat16:
+            assert bool((y.view(torch.int16)[torch.isnan(y)] == 0x7FC0).all()), "non-canonical bf16 NaN"
+        if M % 128 == 0 and N % 384 == 0 and K % 64 == 0:
+            assert_gemm_close_dev(capi_scaled_mm(a, bp, s, bias, out, (2, 4, 4, 4, 6)), ref, out, f"128x384 {case}")
+        del ref, y
