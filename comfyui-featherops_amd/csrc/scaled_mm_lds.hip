@@ -648,7 +648,8 @@ bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
 }
 
 // Split-K plan for M <= 64: a 32- or 64-row tile and enough K splits to give
-// about `target` workgroups (each split keeps at least one 64-K stage).
+// about `target` workgroups (each split keeps at least one 64-K stage; no
+// split below 32 stages).
 // Measured on MI355X (weights rotated past the MALL): 64 x 64 tiles beat
 // 64 x 128 / 64 x 256 at M = 64 for N = 3072..13824, and 32 x 128 is the best
 // 32-row tile (the small-M kernel still wins at M <= 32).
@@ -660,6 +661,10 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
     const int64_t nk = K / kBK;
     int64_t ks = (target + tiles - 1) / tiles;
+    // below 32 stages (K < 2048) the split's partial round trip costs more than the stages it
+    // spreads (measured: M=256 N=K=1024 6.0 us unsplit vs 7.2 us in 4 splits, M=256 N=2048
+    // K=512 4.7 vs 6.7 us; from K=2048 on splitting wins or ties)
+    if (nk < 32) ks = 1;
     if (ks > nk) ks = nk;
     if (ks > 32) ks = 32;
     if (ks < 1) ks = 1;

@@ -285,8 +285,8 @@ def test_workspace_shared_across_shapes(cuda):
     split-K LDS tiles, each shape twice, fewer tiles before more."""
     from gpu_util import lib, stream
 
-    seq = [(16, 3072, 12288), (16, 5120, 13824), (1, 3072, 12288), (256, 1024, 1472), (512, 1072, 1024),
-           (64, 4096, 4096), (48, 12288, 2048), (16, 5120, 13824), (512, 1072, 1024)]
+    seq = [(16, 3072, 12288), (16, 5120, 13824), (1, 3072, 12288), (256, 1024, 2112), (512, 1072, 2048),
+           (64, 4096, 4096), (48, 12288, 2048), (16, 5120, 13824), (512, 1072, 2048)]
     cfg = (2, 2, 4, 4, 4)
     need = max(lib().feather_scaled_mm_workspace_size(M, N, K, *cfg) for M, N, K in seq)
     ws = torch.zeros(need, dtype=torch.uint8, device=cuda)
@@ -498,7 +498,7 @@ def test_baseline_config1_gemm(cuda, hk, quant):
     assert_gemm_close(y, ref, torch.float16, "C1 scaled_mm_hip", literal=True)
     y = hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16)
     assert_gemm_close(y, ref, torch.float16, "C1 any-M", literal=True)
-    # the route BASELINE config 1 takes by default (split-K 64x64 tiles) is deterministic
+    # the route BASELINE config 1 takes by default (the 64x64 split-K-route tiles, unsplit at K=1024) is deterministic
     assert torch.equal(y, hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16))
 
 

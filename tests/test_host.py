@@ -282,7 +282,7 @@ def test_splitk_plan_without_counter_room_needs_no_workspace():
 
     code = ("import __graft_entry__; __graft_entry__.load_package();"
             "from featherops_amd.kernel.hip import _lib; L = _lib.lib();"
-            "print(L.feather_scaled_mm_workspace_size(64, 16400 * 64, 512, 2, 2, 4, 4, 4),"
+            "print(L.feather_scaled_mm_workspace_size(64, 16400 * 64, 2048, 2, 2, 4, 4, 4),"
             " L.feather_scaled_mm_workspace_size(64, 4096, 4096, 2, 2, 4, 4, 4))")
     env = dict(__import__("os").environ, FEATHEROPS_SMALLM_GROUPS="40000")
     out = subprocess.run([sys.executable, "-c", code], cwd=REPO, env=env, capture_output=True, text=True,
