@@ -51,7 +51,7 @@ extern "C" {
  *   has_scale / has_bias: 0 or 1; scale / bias are only read when set.
  *   (block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n): one of the
  *   configurations the reference lists (hip_kernel.py:60-89) or one of the
- *   gfx950 additions (2,4,4,8,4), (4,2,4,4,8), (4,2,4,4,4). The tuple keeps the reference's
+ *   gfx950 additions (2,4,4,8,4), (4,2,4,4,8), (4,2,4,4,4), (2,4,4,8,3), (2,4,4,4,6). The tuple keeps the reference's
  *   divisibility meaning (BlockM = 16*wm*rm, BlockN = 16*wn*rn, ChunkK = 16*u)
  *   for callers that pad to it; the kernels themselves accept any M.
  *   b_dtype: FEATHER_B_E4M3FN or FEATHER_B_E5M2. output_dtype: 0 fp16, 1 bf16.
@@ -172,7 +172,7 @@ size_t feather_lora_down_workspace_size(int64_t M, int64_t K, int64_t R);
 /*
  * A configuration tuple for this shape on the current device, without timing
  * anything: the output tile whose waves of workgroups times tile cost is
- * smallest (256x256, 256x192, 128x256, 256x128 or 128x128; the small-M
+ * smallest (256x256, 256x192, 128x384, 128x256, 256x128 or 128x128; the small-M
  * kernel's tuple for M <= 64). Writes 5 ints (block_warps_m, block_warps_n,
  * unroll_k, repeat_m, repeat_n) to cfg. The tuple ignores the reference's
  * block-divisibility rule (for the any-M entry). No counterpart in the
