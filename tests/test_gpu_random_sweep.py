@@ -175,3 +175,34 @@ def test_random_large_shapes(cuda, hk):
         if M % 128 == 0 and N % 384 == 0 and K % 64 == 0:
             assert_gemm_close_dev(capi_scaled_mm(a, bp, s, bias, out, (2, 4, 4, 4, 6)), ref, out, f"128x384 {case}")
         del ref, y
+
+
+
+def test_random_large_shapes_e4m3_bf16_activations(cuda, hk):
+    """The large-shape sweep with e4m3fn weights and bf16 activations mixed in: the any-M op
+    (bf16 activations are rounded to fp16 by the library's cast, as ops.py:88's x.to(float16))
+    over the whole output against a float64 evaluation of the same fp16 activations."""
+    from gpu_util import assert_gemm_close_dev, torch_ref_dev
+
+    rng = np.random.default_rng(7)
+    gd = torch.Generator(device=cuda).manual_seed(7)
+    for case in range(8):
+        M = int(rng.integers(1000, 5000))
+        N = 384 * int(rng.integers(1, 10)) if rng.random() < 0.5 else 16 * int(rng.integers(20, 600))
+        K = 64 * int(rng.integers(1, 50))
+        out = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+        e4m3 = rng.random() < 0.5
+        a_bf16 = rng.random() < 0.5
+        fmt = torch.float8_e4m3fn if e4m3 else torch.float8_e5m2
+        fmax = 448.0 if e4m3 else 57344.0
+        x = torch.randn(M, K, generator=gd, device=cuda)
+        a = x.to(torch.bfloat16) if a_bf16 else x.half()
+        w = torch.randn(N, K, generator=gd, device=cuda) * 0.02
+        s = (w.abs().max() / fmax).float().reshape(1)
+        bp = (w / s).to(fmt).view(N, K // 16, 16).permute(1, 0, 2).contiguous()
+        bias = (torch.randn(N, generator=gd, device=cuda) * 0.1).to(out)
+        print("large e4m3/bf16", case, M, N, K, out, e4m3, a_bf16, hk.any_m_config(M, N, K), flush=True)
+        ref = torch_ref_dev(a.to(torch.float16), bp, s, bias, out, b_dtype=fmt)
+        y = hk.scaled_mm_hip_any_m(a, bp, s, bias, out)
+        assert_gemm_close_dev(y, ref, out, f"large e4m3/bf16 {case}")
+        del ref, y
