@@ -100,11 +100,17 @@ def lora_factors(x: torch.Tensor, weight_functions, cache: dict | None = None):
 
 def lora_down(x: torch.Tensor, d: torch.Tensor) -> torch.Tensor:
     """T = F.linear(x, d) on the library's skinny-GEMM kernel (torch.ops.feather_ops.lora_down:
-    fp32 accumulation, rounded to x's dtype); torch's F.linear only when K is not a multiple of 8
-    (the kernel's 16-byte row loads) or x is not on the GPU."""
+    fp32 accumulation, rounded to x's dtype); torch's F.linear wherever the kernel's entry would
+    refuse the operands: x not on the GPU, K not a multiple of 8 (16-byte row loads), ranks not a
+    multiple of 32 or above 65536, K >= 2^24, or a storage offset that leaves x or d off a
+    16-byte boundary."""
     x2 = x.reshape(-1, x.shape[-1])
-    if x2.is_cuda and x2.shape[1] % 8 == 0 and d.shape[0] % 32 == 0:
-        _lib.load_torch_ops()
-        t = torch.ops.feather_ops.lora_down.default(x2.contiguous(), d.contiguous())
-        return t.reshape(*x.shape[:-1], d.shape[0])
+    K, R = x2.shape[1], d.shape[0]
+    if x2.is_cuda and K % 8 == 0 and R % 32 == 0 and R <= 65536 and K < (1 << 24):
+        x2 = x2.contiguous()
+        dc = d.contiguous()
+        if x2.data_ptr() % 16 == 0 and dc.data_ptr() % 16 == 0:
+            _lib.load_torch_ops()
+            t = torch.ops.feather_ops.lora_down.default(x2, dc)
+            return t.reshape(*x.shape[:-1], R)
     return F.linear(x, d).contiguous()

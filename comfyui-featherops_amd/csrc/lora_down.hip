@@ -150,7 +150,9 @@ __global__ __launch_bounds__(64 * WM * WN) void lora_down_kernel(const uint16_t*
     };
 
     // three-stage ring: copies of stages st + 1 and st + 2 in flight while st is multiplied
-    issue_stage(0, 0);
+    // (the planner gives every split at least one stage; the guard keeps an
+    // empty split's copies from reading past the ends of x and D regardless)
+    if (nst > 0) issue_stage(0, 0);
     if (nst > 1) issue_stage(1, 1);
     for (int st = 0; st < nst; ++st) {
         if (st + 1 < nst) wait_vmcnt<kLoads>();
@@ -257,7 +259,13 @@ int lora_ksplit(int64_t M, int64_t K, int nchunks) {
     int64_t ks = (256 + tiles - 1) / tiles;
     if (ks > nst / 2) ks = nst / 2;
     if (ks > 16) ks = 16;
-    return ks < 1 ? 1 : static_cast<int>(ks);
+    if (ks <= 1) return 1;
+    // the kernel gives split q the stages [q * per, min((q + 1) * per, nst)):
+    // drop trailing splits that would own none (K = 4160: 65 stages, 16 splits
+    // of 5 cover them with 13)
+    const int64_t per = (nst + ks - 1) / ks;
+    ks = (nst + per - 1) / per;
+    return static_cast<int>(ks);
 }
 
 size_t chunk_workspace(int64_t M, int64_t K, const LoraChunk& c) {

@@ -114,7 +114,10 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
  * counters and fp32 partials) is a static device array of
  * FEATHER_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the
  * first call on a device looks up its address (hipGetSymbolAddress) and
- * clears its counters with a fill kernel on `stream`. Results equal
+ * clears its counters with a fill kernel on `stream`, so that first call on
+ * each device must be made eagerly, outside stream capture (the symbol lookup
+ * may be refused during capture, and the fill would be recorded into the
+ * caller's graph); later calls may be captured. Results equal
  * feather_launch_scaled_mm_ex with a caller workspace of the size
  * feather_scaled_mm_workspace_size reports. Every call on a GPU shares that
  * GPU's array: calls that overlap on one GPU (other streams, other threads)

@@ -36,7 +36,8 @@ def _capi(x, d, split=True):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,K,R", [(1, 8, 32), (17, 24, 64), (300, 1040, 96), (256, 3072, 128), (40, 520, 160),
-                                   (129, 2048, 256), (8200, 64, 32), (4096, 3072, 64)])
+                                   (129, 2048, 256), (8200, 64, 32), (4096, 3072, 64),
+                                   (1, 4160, 32), (1, 520, 32), (70, 4160, 128)])
 def test_lora_down_vs_oracle(cuda, hk, dtype, M, K, R):
     g = torch.Generator().manual_seed(M + K + R)
     x = torch.randn(M, K, generator=g).to(dtype)
@@ -134,3 +135,22 @@ def test_lora_down_graph_replays_match_eager(cuda, hk):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {rep}"
         assert torch.isfinite(junk)
+
+
+def test_lora_down_python_entry_falls_back_on_misaligned_x(cuda, hk, pkg):
+    """comfy_feather.lora.lora_down takes torch's F.linear where the kernel's entry would refuse
+    the operands (here: x at a storage offset of one element, off the 16-byte boundary) instead
+    of raising; aligned x goes to the kernel and agrees with the oracle."""
+    from featherops_amd.comfy_feather import lora
+
+    M, K, R = 33, 256, 32
+    g = torch.Generator().manual_seed(7)
+    buf = torch.randn(M * K + 1, generator=g).half().to(cuda)
+    d = (torch.randn(R, K, generator=g) * 0.05).half().to(cuda)
+    x_off = buf[1:].view(M, K)
+    assert x_off.data_ptr() % 16 != 0
+    t_off = lora.lora_down(x_off, d)
+    assert torch.equal(t_off, F.linear(x_off, d).contiguous())
+    x_al = x_off.clone()
+    t_al = lora.lora_down(x_al, d)
+    assert_gemm_close(t_al, O.lora_down_ref(_np(x_al), _np(d), O.DT_F16), torch.float16, "aligned x")

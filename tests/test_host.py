@@ -290,3 +290,31 @@ def test_splitk_plan_without_counter_room_needs_no_workspace():
     assert out.returncode == 0, out.stderr
     big, small = map(int, out.stdout.split())
     assert big == 0 and small > 0
+
+
+def test_lora_down_plan_leaves_no_split_empty(pkg):
+    """The LoRA down-projection splits K across workgroups (split q owns stages
+    [q * per, min((q + 1) * per, nst)) of 64 K): every split must own at least one
+    stage, else its prologue copies would address past the ends of x and D. The
+    split count is read back from the workspace size (counters + tiles x splits
+    fp32 partial tiles of 64 rows x R ranks)."""
+    from featherops_amd.kernel.hip import _lib
+
+    L = _lib.lib()
+    checked = 0
+    for M, R in ((1, 32), (40, 128), (200, 64)):
+        tiles = (M + 63) // 64
+        for K in range(8, 20001, 8):
+            ws = L.feather_lora_down_workspace_size(M, K, R)
+            nst = (K + 63) // 64
+            if ws == 0:
+                assert nst < 4  # no split below two stages per split
+                continue
+            part = tiles * 64 * R * 4
+            assert (ws - 65536) % part == 0
+            ks = (ws - 65536) // part
+            per = -(-nst // ks)
+            assert 2 <= ks <= 16 and ks <= nst // 2
+            assert (ks - 1) * per < nst, (M, K, R, ks, per, nst)
+            checked += 1
+    assert checked > 7000
