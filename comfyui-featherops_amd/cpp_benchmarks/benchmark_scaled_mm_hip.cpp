@@ -18,6 +18,12 @@
 // --lora-down R: time feather_lora_down instead, T (M x R) = x (M x K) . D^T
 // with bf16 x ~ U[-1, 1) rotated over --rotate buffers and D (R x K), GB/s on
 // the bytes of x, D and T.
+// --convert rtz|rne: time feather_bf16_to_fp16 (round toward zero, the
+// reference's kernel/convert.py) or feather_bf16_to_fp16_rne on an N x N bf16
+// matrix (randn), GB/s on 4 bytes per element (2 read + 2 written), the
+// reference benchmark_convert.py's measure; --rotate buffers in and out.
+// --dequant: time feather_dequantize_e5m2 of an (K/16, N, 16) e5m2 weight to an
+// N x K fp16 matrix, GB/s on 3 bytes per element (1 read + 2 written).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -55,13 +61,15 @@ struct Opts {
     int rotate = 1;
     bool quant = false;
     int64_t lora_rank = 0;
+    int convert = 0;  // 1 rtz, 2 rne
+    bool dequant = false;
 };
 
 void usage(const char* argv0) {
     std::cout << "Usage: " << argv0
               << " [--m M] [--n N] [--k K] [--warmup W] [--iters I] [--warps_m M] [--warps_n N] [--unroll U]"
                  " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant]"
-                 " [--lora-down R]\n";
+                 " [--lora-down R] [--convert rtz|rne] [--dequant]\n";
 }
 
 Opts parse(int argc, char** argv) {
@@ -90,6 +98,8 @@ Opts parse(int argc, char** argv) {
         else if (a == "--rotate") o.rotate = std::max(1, std::stoi(val()));
         else if (a == "--quant") o.quant = true;
         else if (a == "--lora-down") o.lora_rank = std::stoll(val());
+        else if (a == "--convert") o.convert = val() == "rne" ? 2 : 1;
+        else if (a == "--dequant") o.dequant = true;
         else if (a == "--help" || a == "-h") {
             usage(argv[0]);
             std::exit(0);
@@ -233,11 +243,97 @@ int run_lora_down(const Opts& o) {
     return 0;
 }
 
+// One HBM-bound auxiliary kernel, back to back over o.rotate (input, output)
+// pairs: --convert (bf16 -> fp16 of an N x N matrix) or --dequant (an N x K
+// e5m2 weight to fp16).
+int run_aux(const Opts& o) {
+    const bool conv = o.convert != 0;
+    const size_t n = conv ? static_cast<size_t>(o.n) * o.n : static_cast<size_t>(o.n) * o.k;
+    const size_t in_bytes = conv ? 2 * n : n;
+    const size_t out_bytes = 2 * n;
+    std::mt19937 gen(42);
+    std::vector<uint8_t> host(in_bytes);
+    if (conv) {
+        std::normal_distribution<float> nrm(0.f, 1.f);
+        for (size_t i = 0; i < n; ++i) {
+            const uint16_t b = to_bf16_bits(nrm(gen));
+            std::memcpy(&host[2 * i], &b, 2);
+        }
+    } else {
+        // e5m2 codes of finite values (exponent field below 31)
+        std::uniform_int_distribution<int> code(0, 255);
+        for (auto& c : host) {
+            int v = code(gen);
+            if ((v & 0x7c) == 0x7c) v &= 0xbb;
+            c = static_cast<uint8_t>(v);
+        }
+    }
+    std::vector<void*> din(o.rotate), dout(o.rotate);
+    for (int i = 0; i < o.rotate; ++i) {
+        HIP_OK(hipMalloc(&din[i], in_bytes));
+        HIP_OK(hipMemcpy(din[i], host.data(), in_bytes, hipMemcpyHostToDevice));
+        HIP_OK(hipMalloc(&dout[i], out_bytes));
+    }
+    float* dscale;
+    HIP_OK(hipMalloc(&dscale, sizeof(float)));
+    const float hs = 0.0125f;
+    HIP_OK(hipMemcpy(dscale, &hs, sizeof(float), hipMemcpyHostToDevice));
+    hipStream_t stream;
+    hipEvent_t t0, t1;
+    HIP_OK(hipStreamCreate(&stream));
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+    auto run = [&](int i) {
+        const int j = i % o.rotate;
+        int rc;
+        if (o.convert == 1)
+            rc = feather_bf16_to_fp16(static_cast<const uint16_t*>(din[j]), static_cast<uint16_t*>(dout[j]), n, stream);
+        else if (o.convert == 2)
+            rc = feather_bf16_to_fp16_rne(static_cast<const uint16_t*>(din[j]), static_cast<uint16_t*>(dout[j]), n,
+                                          stream);
+        else
+            rc = feather_dequantize_e5m2(static_cast<const uint8_t*>(din[j]), dscale, dout[j], FEATHER_DTYPE_F16, o.n,
+                                         o.k, stream);
+        if (rc != FEATHER_OK) {
+            std::cerr << "launch failed: " << feather_status_string(rc) << std::endl;
+            std::exit(1);
+        }
+    };
+    for (int i = 0; i < o.warmup; ++i) run(i);
+    HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipEventRecord(t0, stream));
+    for (int i = 0; i < o.iters; ++i) run(i);
+    HIP_OK(hipEventRecord(t1, stream));
+    HIP_OK(hipEventSynchronize(t1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+    ms /= o.iters;
+    const double bytes = static_cast<double>(in_bytes + out_bytes);
+    std::cout << std::fixed << std::setprecision(4);
+    if (conv)
+        std::cout << "bf16_to_fp16" << (o.convert == 2 ? "_rne" : "") << " benchmark\n  problem: n=" << o.n
+                  << " (n x n) rotate=" << o.rotate;
+    else
+        std::cout << "dequantize_e5m2 benchmark\n  problem: n=" << o.n << " k=" << o.k << " fp16 out rotate=" << o.rotate;
+    std::cout << "\n  back-to-back us: " << ms * 1e3 << "  (GB/s " << bytes / ms / 1e6 << " on " << (conv ? 4 : 3)
+              << " B/element)" << std::endl;
+    for (int i = 0; i < o.rotate; ++i) {
+        HIP_OK(hipFree(din[i]));
+        HIP_OK(hipFree(dout[i]));
+    }
+    HIP_OK(hipFree(dscale));
+    HIP_OK(hipEventDestroy(t0));
+    HIP_OK(hipEventDestroy(t1));
+    HIP_OK(hipStreamDestroy(stream));
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     const Opts o = parse(argc, argv);
     if (o.quant) return run_quant(o);
+    if (o.convert || o.dequant) return run_aux(o);
     if (o.lora_rank > 0) return run_lora_down(o);
     if (o.k % (16 * o.u) != 0) {
         std::cerr << "K must be divisible by 16 * unroll_k (" << 16 * o.u << ")" << std::endl;
@@ -337,6 +433,7 @@ int main(int argc, char** argv) {
     std::cout << "  avg GB/s: " << bytes / avg / 1e6 << "\n";
     std::cout << "  back-to-back ms: " << stream_ms << "  (TFLOP/s " << flops / stream_ms / 1e9 << ", GB/s "
               << bytes / stream_ms / 1e6 << ")" << std::endl;
+    std::cout << "  back-to-back us: " << stream_ms * 1e3 << std::endl;
 
     HIP_OK(hipEventDestroy(t0));
     HIP_OK(hipEventDestroy(t1));
