@@ -535,3 +535,58 @@ def test_multi_wave_grids_ragged(cuda, M, N, K, out_dtype):
                                              ws.data_ptr(), nbytes, stream(cuda))
         torch.cuda.synchronize()
         assert torch.equal(y2.view(torch.int16), first.view(torch.int16)), f"{cfg} workspace entry differs"
+
+
+def _lean_call(ad, bd, sd, bsd, M, N, K, a_bf16, b_e4m3, out_dtype, has_scale=1, has_bias=1):
+    c = torch.full((M, N), float("nan"), dtype=out_dtype, device=ad.device)
+    ok = lib().feather_launch_scaled_mm_ex(ad.data_ptr(), int(a_bf16), bd.data_ptr(),
+                                           sd.data_ptr() if has_scale else None,
+                                           bsd.data_ptr() if has_bias else None, c.data_ptr(), M, N, K, has_scale,
+                                           has_bias, 1, 1, 2, 1, 2, 0 if b_e4m3 else 1,
+                                           0 if out_dtype == torch.float16 else 1, None, 0, stream(ad.device))
+    assert ok
+    torch.cuda.synchronize()
+    return c
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 16])
+@pytest.mark.parametrize("variant", ["f16_e5m2_f16", "f16_e4m3_bf16", "bf16_e5m2_f16", "bf16_e5m2_bf16",
+                                     "noscale_nobias"])
+def test_small_m_lean_route(cuda, M, variant):
+    """M <= 16 with K % 64 == 0 and one K range per 16-column strip runs the lean small-M
+    kernel, which copies only the A rows below M into LDS: rows >= M of its LDS slabs hold
+    whatever the previous workgroup on that CU left there. A call with M = 16 and an all-NaN
+    A runs first on the same shape, so every slab row past M holds NaN bits when the M-row
+    call runs; its output must still equal the oracle (an output row reads only its own A
+    row) and carry no NaN."""
+    N, K = 4096, 2048
+    a_bf16 = variant.startswith("bf16")
+    b_e4m3 = "e4m3" in variant
+    out_dtype = torch.bfloat16 if variant.endswith("bf16") else torch.float16
+    has_scale = has_bias = 0 if variant == "noscale_nobias" else 1
+    g = torch.Generator().manual_seed(1000 + M)
+    a = torch.randn(M, K, generator=g)
+    if not has_scale:
+        a = a * 1e-3  # unscaled codes reach 57344: keep |C| far below fp16's range
+    a_t = a.bfloat16() if a_bf16 else a.half()
+    if b_e4m3:
+        w = torch.randn(N, K, generator=g) * 0.02
+        s = np.float32(w.abs().max().item()) / np.float32(448.0)
+        codes = (w * float(np.float32(1.0) / s)).to(torch.float8_e4m3fn).view(torch.uint8)
+        packed = codes.view(N, K // 16, 16).permute(1, 0, 2).contiguous().numpy()
+        bd = to_dev_codes(packed, cuda, torch.float8_e4m3fn)
+    else:
+        packed, s = weight_like(N, K, g)
+        bd = to_dev_codes(packed, cuda)
+    bias, bias_np = _bias_for(out_dtype, N, g)
+    sd = torch.tensor([s], device=cuda)
+    bsd = bias.to(cuda)
+    # fill the LDS slabs with NaN rows: an M = 16 call on an all-NaN A of the same dtype
+    poison = torch.full((16, K), float("nan"), dtype=a_t.dtype, device=cuda)
+    yp = _lean_call(poison, bd, sd, bsd, 16, N, K, a_bf16, b_e4m3, out_dtype)
+    assert torch.isnan(yp).all()
+    y = _lean_call(a_t.to(cuda), bd, sd, bsd, M, N, K, a_bf16, b_e4m3, out_dtype, has_scale, has_bias)
+    od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
+    ref = O.scaled_mm_ref(a_t.to(torch.float16).numpy(), packed, s if has_scale else None,
+                          bias_np if has_bias else None, od, "e4m3fn" if b_e4m3 else "e5m2")
+    assert_gemm_close(y, ref, out_dtype, f"lean {variant} M={M}")
