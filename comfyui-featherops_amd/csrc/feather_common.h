@@ -176,21 +176,23 @@ __device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast
 // same values as torch's x.to(float16) that the reference's Linear applies
 // before the GEMM (comfy_feather/ops.py:88). bf16 -> fp32 is exact (a shift);
 // v_cvt_pk_f16_f32 rounds two fp32 values to fp16 at once.
+// Two packed bf16 values -> two packed fp16 values, round to nearest even
+// (the values of torch's x.to(float16): exact widening to fp32, one rounding).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2_rne(uint32_t w) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f32x2 f = {bits_f32(w << 16), bits_f32(w & 0xffff0000u)};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+}
+
 template <bool kABf16>
 __device__ __forceinline__ half8_t a_frag(uint4 v) {
     if constexpr (!kABf16) {
         return as_half8(v);
     } else {
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
-        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f32x2 f = {bits_f32(w[i] << 16), bits_f32(w[i] & 0xffff0000u)};
-            o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
-        }
-        return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+        const uint4 o = make_uint4(bf16x2_to_f16x2_rne(v.x), bf16x2_to_f16x2_rne(v.y), bf16x2_to_f16x2_rne(v.z),
+                                   bf16x2_to_f16x2_rne(v.w));
+        return __builtin_bit_cast(half8_t, o);
     }
 }
 

@@ -308,7 +308,8 @@ def test_workspace_shared_across_shapes(cuda):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (16, 12288, 512), (48, 1024, 2048), (64, 1024, 1024),
-                                   (256, 768, 512), (1024, 4096, 1024), (100, 512, 1040)])
+                                   (256, 768, 512), (1024, 4096, 1024), (100, 512, 1040), (4096, 4096, 4096),
+                                   (4096, 3072, 3072), (1000, 5120, 640), (4608, 3072, 3072)])
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
 def test_bf16_activations(cuda, hk, M, N, K, out_dtype):
     """bf16 A through the any-M entry: rounded to fp16 inside the kernel (or cast
