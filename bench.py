@@ -101,16 +101,18 @@ def time_steady(fn, min_calls: int = 3, window_ms: float = 25.0):
     return time_launches(fn, n)
 
 
-def streaming_floor_us(nbytes: int):
+def streaming_floor_us(nbytes: int, graph: bool = False):
     """Per-call time of a plain read-only streaming kernel over nbytes (24 rotated buffers),
-    measured by the C++ bench in a child process; None if it is not built."""
+    measured by the C++ bench in a child process (back-to-back launches, or with graph=True
+    the 24 launches replayed from a HIP graph); None if it is not built."""
     import subprocess
 
     exe = REPO / "comfyui-featherops_amd" / "cpp_benchmarks" / "build" / "benchmark_hbm_copy"
     if not exe.exists():
         return None
     try:
-        out = subprocess.run([str(exe), "--read-bytes", str(nbytes)], capture_output=True, text=True, timeout=120)
+        out = subprocess.run([str(exe), "--read-bytes", str(nbytes)] + (["--graph"] if graph else []),
+                             capture_output=True, text=True, timeout=120)
     except (OSError, subprocess.TimeoutExpired):
         return None
     m = re.search(r"([0-9.]+) us/call", out.stdout)
@@ -118,9 +120,10 @@ def streaming_floor_us(nbytes: int):
 
 
 def cpp_bench_us(M: int, N: int, K: int, rotate: int = 24, iters: int = 5000):
-    """Per-call time of back-to-back launches of the small-M GEMM through the C ABI
-    (cpp_benchmarks/benchmark_scaled_mm_hip, rotate distinct weights, fp16 out, scale and
-    bias): the same launch method as streaming_floor_us; None if it is not built."""
+    """Per-call times of the small-M GEMM through the C ABI (cpp_benchmarks/benchmark_scaled_mm_hip,
+    rotate distinct weights, fp16 out, scale and bias): (back-to-back launches, the rotate launches
+    replayed from a HIP graph) -- the two launch methods streaming_floor_us offers; None if the
+    bench is not built."""
     import subprocess
 
     exe = REPO / "comfyui-featherops_amd" / "cpp_benchmarks" / "build" / "benchmark_scaled_mm_hip"
@@ -133,7 +136,10 @@ def cpp_bench_us(M: int, N: int, K: int, rotate: int = 24, iters: int = 5000):
     except (OSError, subprocess.TimeoutExpired):
         return None
     m = re.search(r"back-to-back us: ([0-9.]+)", out.stdout)
-    return float(m.group(1)) if out.returncode == 0 and m else None
+    mg = re.search(r"graph-replay us: ([0-9.]+)", out.stdout)
+    if out.returncode != 0 or not m or not mg:
+        return None
+    return float(m.group(1)), float(mg.group(1))
 
 
 def _cpp_bench(args, key: str, timeout: int = 180):
@@ -624,14 +630,23 @@ def main() -> int:
             result["small_m"]["floor"] = ("read-only streaming kernel over the same byte count, 24 rotated buffers, "
                                           "back to back (cpp_benchmarks/benchmark_hbm_copy --read-bytes)")
             log(f"bench: streaming floor for {gemm_bytes(Ms, Ns, Ks)} B: {floor:.2f} us/call")
-        b2b = cpp_bench_us(Ms, Ns, Ks, nrot)
-        if b2b is not None:
-            # the floor is timed as back-to-back launches from C++; the same method for the GEMM
-            # gives the like-for-like ratio (a HIP-graph replay adds per-node overhead)
+        floor_g = streaming_floor_us(gemm_bytes(Ms, Ns, Ks), graph=True)
+        if floor_g is not None:
+            # the same floor with its 24 launches replayed from a HIP graph
+            result["small_m"]["floor_graph_us"] = round(floor_g, 3)
+            log(f"bench: streaming floor, graph replay: {floor_g:.2f} us/call")
+        cpp = cpp_bench_us(Ms, Ns, Ks, nrot)
+        if cpp is not None:
+            # the floor's two launch methods applied to the GEMM through the C ABI: the like-for-like
+            # ratios (torch's graph replay above adds ~0.5 us per node over a plain HIP graph)
+            b2b, gr = cpp
             result["small_m"]["back_to_back_us_per_call"] = round(b2b, 3)
+            result["small_m"]["hip_graph_us_per_call"] = round(gr, 3)
             if floor is not None:
                 result["small_m"]["frac_of_floor_back_to_back"] = round(floor / b2b, 3)
-            log(f"bench: small-M back-to-back launches (C++, same method as the floor) {b2b:.2f} us/call")
+            if floor_g is not None:
+                result["small_m"]["frac_of_floor_hip_graph"] = round(floor_g / gr, 3)
+            log(f"bench: small-M through the C ABI: back to back {b2b:.2f} us/call, HIP graph {gr:.2f} us/call")
 
         # ---------------- quantize + prepack (config 5's on-device op) ----------------
         # four distinct 141.6 MB weights (566 MB) in rotation, so the weight is streamed from HBM

@@ -9,6 +9,9 @@
 //       Infinity Cache cannot serve them: the per-call floor a weight-streaming
 //       kernel of that size can reach (launch + ramp + drain included)
 //   benchmark_hbm_copy --read-bytes B  the same floor for one size of B bytes
+//   benchmark_hbm_copy --read-bytes B --graph  the same 24 launches captured
+//       once in a HIP graph and replayed (the launch method of a graph-replay
+//       timing of the GEMM)
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -45,7 +48,7 @@ __global__ __launch_bounds__(256) void read16(const uint4* __restrict__ src, int
     if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live
 }
 
-int read_sweep(const std::initializer_list<int64_t>& sizes) {
+int read_sweep(const std::initializer_list<int64_t>& sizes, bool graph = false) {
     const int nbuf = 24;
     uint32_t* sink;
     HIP_OK(hipMalloc(&sink, 4));
@@ -64,15 +67,40 @@ int read_sweep(const std::initializer_list<int64_t>& sizes) {
         for (int i = 0; i < nbuf; ++i)
             hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, 0, static_cast<const uint4*>(bufs[i]), n, sink);
         HIP_OK(hipDeviceSynchronize());
-        HIP_OK(hipEventRecord(t0, 0));
-        for (int i = 0; i < 10 * nbuf; ++i)
-            hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, 0, static_cast<const uint4*>(bufs[i % nbuf]), n, sink);
-        HIP_OK(hipEventRecord(t1, 0));
-        HIP_OK(hipEventSynchronize(t1));
         float ms = 0.f;
-        HIP_OK(hipEventElapsedTime(&ms, t0, t1));
-        ms /= 10 * nbuf;
-        std::cout << "read " << bytes << " B: " << ms * 1000.0 << " us/call, " << bytes / ms / 1e6 << " GB/s" << std::endl;
+        if (graph) {
+            hipStream_t s;
+            HIP_OK(hipStreamCreate(&s));
+            hipGraph_t g;
+            hipGraphExec_t ge;
+            HIP_OK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            for (int i = 0; i < nbuf; ++i)
+                hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, s, static_cast<const uint4*>(bufs[i]), n, sink);
+            HIP_OK(hipStreamEndCapture(s, &g));
+            HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+            for (int r = 0; r < 10; ++r) HIP_OK(hipGraphLaunch(ge, s));
+            HIP_OK(hipStreamSynchronize(s));
+            HIP_OK(hipEventRecord(t0, s));
+            for (int r = 0; r < 40; ++r) HIP_OK(hipGraphLaunch(ge, s));
+            HIP_OK(hipEventRecord(t1, s));
+            HIP_OK(hipEventSynchronize(t1));
+            HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+            ms /= 40 * nbuf;
+            HIP_OK(hipGraphExecDestroy(ge));
+            HIP_OK(hipGraphDestroy(g));
+            HIP_OK(hipStreamDestroy(s));
+        } else {
+            HIP_OK(hipEventRecord(t0, 0));
+            for (int i = 0; i < 10 * nbuf; ++i)
+                hipLaunchKernelGGL(read16, dim3(grid), dim3(256), 0, 0, static_cast<const uint4*>(bufs[i % nbuf]), n,
+                                   sink);
+            HIP_OK(hipEventRecord(t1, 0));
+            HIP_OK(hipEventSynchronize(t1));
+            HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+            ms /= 10 * nbuf;
+        }
+        std::cout << "read " << bytes << " B" << (graph ? " (graph replay)" : "") << ": " << ms * 1000.0
+                  << " us/call, " << bytes / ms / 1e6 << " GB/s" << std::endl;
         for (auto& b : bufs) HIP_OK(hipFree(b));
     }
     HIP_OK(hipFree(sink));
@@ -91,7 +119,8 @@ int main(int argc, char** argv) {
                 std::cerr << "--read-bytes takes 1 .. 2^32" << std::endl;
                 return 1;
             }
-            return read_sweep({b});
+            const bool graph = i + 1 < argc && std::string(argv[i + 1]) == "--graph";
+            return read_sweep({b}, graph);
         }
         if (i + 1 >= argc) break;
         if (a == "--mib") mib = std::stoll(argv[++i]);

@@ -434,6 +434,27 @@ int main(int argc, char** argv) {
     std::cout << "  back-to-back ms: " << stream_ms << "  (TFLOP/s " << flops / stream_ms / 1e9 << ", GB/s "
               << bytes / stream_ms / 1e6 << ")" << std::endl;
     std::cout << "  back-to-back us: " << stream_ms * 1e3 << std::endl;
+    if (o.rotate > 1) {
+        // the rotate launches captured once in a HIP graph and replayed
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+        for (int i = 0; i < o.rotate; ++i) run(i);
+        HIP_OK(hipStreamEndCapture(stream, &g));
+        HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        const int reps = std::max(1, o.iters / o.rotate);
+        for (int r = 0; r < std::max(1, reps / 4); ++r) HIP_OK(hipGraphLaunch(ge, stream));
+        HIP_OK(hipStreamSynchronize(stream));
+        HIP_OK(hipEventRecord(t0, stream));
+        for (int r = 0; r < reps; ++r) HIP_OK(hipGraphLaunch(ge, stream));
+        HIP_OK(hipEventRecord(t1, stream));
+        HIP_OK(hipEventSynchronize(t1));
+        float gms = 0.f;
+        HIP_OK(hipEventElapsedTime(&gms, t0, t1));
+        std::cout << "  graph-replay us: " << gms * 1e3 / (reps * o.rotate) << std::endl;
+        HIP_OK(hipGraphExecDestroy(ge));
+        HIP_OK(hipGraphDestroy(g));
+    }
 
     HIP_OK(hipEventDestroy(t0));
     HIP_OK(hipEventDestroy(t1));
