@@ -241,11 +241,12 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
         __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Lean variant for the most common small-M call: M <= 16, K % 64 == 0, one
-// 16-column strip per workgroup with the whole K range (no split across
-// workgroups). Same arithmetic and summation order as scaled_mm_smallm_kernel
-// with MT = CT = 1 (wave w multiplies stages w, w + 16, ... in order, the 16
-// waves' sums are added in wave order), with less work around the stream:
+// Lean variant for the most common small-M calls: M <= 32 (MT = 1 or 2 row
+// tiles of 16), K % 64 == 0, one 16-column strip per workgroup with the whole
+// K range (no split across workgroups). Same arithmetic and summation order as
+// scaled_mm_smallm_kernel with CT = 1 and the same MT (wave w multiplies
+// stages w, w + 16, ... in order, the 16 waves' sums are added in wave
+// order), with less work around the stream:
 //   * scale and the strip's 16 bias values are read before the first copy
 //     is issued, so the epilogue waits on nothing in memory;
 //   * each stage is one copy instruction of A per 8 rows (only rows < M are
@@ -256,17 +257,18 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_smallm_kernel(
 //     measured ~0.4 us slower at M=16, K=N=4096).
 // M=16, K=N=4096, 24 rotated weights, back-to-back launches: 5.87 us against
 // 6.45 us for the general kernel on the same box.
-template <bool kBf16, bool kE4m3, bool kABf16>
+template <int MT, bool kBf16, bool kE4m3, bool kABf16>
 __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16_t* __restrict__ A,
                                                                      const uint8_t* __restrict__ Bp,
                                                                      const float* __restrict__ scale,
                                                                      const uint16_t* __restrict__ bias,
                                                                      uint16_t* __restrict__ C, int M, int N, int K,
                                                                      int has_scale, int has_bias) {
-    constexpr int U = 4;  // stages in flight per wave
+    constexpr int U = 4 / MT;  // stages in flight per wave (the slabs fill 128 KB of LDS)
+    constexpr int kStageSlab = MT * kSlabTile;
     constexpr int kRedStride = 17;
-    static_assert(kWaves * 16 * kRedStride * 4 <= kWaves * U * kSlabTile, "reduction fits the slabs");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kWaves * U * kSlabTile];
+    static_assert(kWaves * 16 * MT * kRedStride * 4 <= kWaves * U * kStageSlab, "reduction fits the slabs");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kWaves * U * kStageSlab];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -277,19 +279,22 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
 
     const float s = has_scale ? scale[0] : 1.0f;
     // lane c < 16 of every wave holds the bias of column n0 + c (read by the
-    // first four waves' epilogue lanes through a shuffle)
+    // epilogue lanes through a shuffle)
     const uint16_t bias_c = has_bias && lane < 16 ? bias[n0 + lane] : static_cast<uint16_t>(0);
 
-    // copy j of a stage: rows 8 j .. 8 j + 7, lane -> (row 8 j + lane / 8, chunk lane % 8)
+    // copy j of a stage: rows 8 j .. 8 j + 7, lane -> (row 8 j + lane / 8, chunk lane % 8);
+    // the swizzle depends on row % 16 only
     const int crow = lane >> 3;
-    const uint32_t cchunk = static_cast<uint32_t>(((lane & 7) ^ swz(crow)) * 16);
+    const uint32_t cchunk0 = static_cast<uint32_t>(((lane & 7) ^ swz(crow)) * 16);
     const uint32_t cchunk1 = static_cast<uint32_t>(((lane & 7) ^ swz(crow + 8)) * 16);
-    const uint32_t slab = lds_addr_of(smem) + wave * (U * kSlabTile);
-    const uint8_t* myslab = smem + wave * (U * kSlabTile);
+    const uint32_t slab = lds_addr_of(smem) + wave * (U * kStageSlab);
+    const uint8_t* myslab = smem + wave * (U * kStageSlab);
     const uint8_t* bcol = Bp + (static_cast<int64_t>(lg) * N + n0 + lr) * 16;
     const int64_t kg_stride = static_cast<int64_t>(N) * 16;  // bytes per K-group row of Bp
 
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int base = wave; base < nst; base += kWaves * U) {
         if (base > wave) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): last round's slab reads done
 #pragma unroll
@@ -297,12 +302,14 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
             const int st = base + u * kWaves;
             if (st < nst) {
                 const uint32_t koff = static_cast<uint32_t>(st) * 128u;
-                if (crow < M)
-                    dma16_lds(A, static_cast<uint32_t>(crow) * static_cast<uint32_t>(K) * 2u + koff + cchunk,
-                              slab + u * kSlabTile);
-                if (M > 8 && crow + 8 < M)
-                    dma16_lds(A, static_cast<uint32_t>(crow + 8) * static_cast<uint32_t>(K) * 2u + koff + cchunk1,
-                              slab + u * kSlabTile + 1024);
+#pragma unroll
+                for (int j = 0; j < 2 * MT; ++j) {
+                    const int row = 8 * j + crow;
+                    if (8 * j < M && row < M)
+                        dma16_lds(A, static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + koff +
+                                         ((j & 1) ? cchunk1 : cchunk0),
+                                  slab + u * kStageSlab + j * 1024);
+                }
             }
         }
         uint4 braw[U];
@@ -316,11 +323,16 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (base + u * kWaves < nst) {
-                const uint8_t* sl = myslab + u * kSlabTile + lr * 128;
-                const uint4 a0 = *reinterpret_cast<const uint4*>(sl + (((2 * lg) ^ swz(lr)) << 4));
-                const uint4 a1 = *reinterpret_cast<const uint4*>(sl + (((2 * lg + 1) ^ swz(lr)) << 4));
-                acc = mfma16x16x32(widen_fp8x8<kE4m3>(braw[u].x, braw[u].y), a_frag<kABf16>(a0), acc);
-                acc = mfma16x16x32(widen_fp8x8<kE4m3>(braw[u].z, braw[u].w), a_frag<kABf16>(a1), acc);
+                const half8_t b0 = widen_fp8x8<kE4m3>(braw[u].x, braw[u].y);
+                const half8_t b1 = widen_fp8x8<kE4m3>(braw[u].z, braw[u].w);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const uint8_t* sl = myslab + u * kStageSlab + t * kSlabTile + lr * 128;
+                    const uint4 a0 = *reinterpret_cast<const uint4*>(sl + (((2 * lg) ^ swz(lr)) << 4));
+                    const uint4 a1 = *reinterpret_cast<const uint4*>(sl + (((2 * lg + 1) ^ swz(lr)) << 4));
+                    acc[t] = mfma16x16x32(b0, a_frag<kABf16>(a0), acc[t]);
+                    acc[t] = mfma16x16x32(b1, a_frag<kABf16>(a1), acc[t]);
+                }
             }
         }
     }
@@ -328,14 +340,16 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     __syncthreads();  // the reduction buffer overlays other waves' slabs
     float* red = reinterpret_cast<float*>(smem);  // [wave][row][kRedStride]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 16 + lr) * kRedStride + 4 * lg + i] = acc[i];
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * 16 * MT + t * 16 + lr) * kRedStride + 4 * lg + i] = acc[t][i];
     __syncthreads();
-    if (tid < 256) {
+    if (tid < 256 * MT) {
         const int r = tid >> 4;
         const int c = tid & 15;
         float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) sum += red[(w * 16 + r) * kRedStride + c];
+        for (int w = 0; w < kWaves; ++w) sum += red[(w * 16 * MT + r) * kRedStride + c];
         const uint16_t b = static_cast<uint16_t>(__shfl(static_cast<int>(bias_c), c));
         if (r < M) {
             uint16_t o = f32_to_out_bits<kBf16>(opaque_f32(sum * s));
@@ -345,12 +359,14 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     }
 }
 
+template <int MT>
 bool launch_m16(const MmArgs& p, hipStream_t stream) {
     const dim3 grid(static_cast<uint32_t>(p.N / 16));
     const dim3 block(64 * kWaves);
-#define FEATHER_M16_LAUNCH(BF, E4, AB)                                                                            \
-    hipLaunchKernelGGL((scaled_mm_m16_kernel<BF, E4, AB>), grid, block, 0, stream, p.a, p.b, p.scale, p.bias, p.c, \
-                       static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K), p.has_scale, p.has_bias)
+#define FEATHER_M16_LAUNCH(BF, E4, AB)                                                                             \
+    hipLaunchKernelGGL((scaled_mm_m16_kernel<MT, BF, E4, AB>), grid, block, 0, stream, p.a, p.b, p.scale, p.bias, \
+                       p.c, static_cast<int>(p.M), static_cast<int>(p.N), static_cast<int>(p.K), p.has_scale,       \
+                       p.has_bias)
     if (p.a_bf16) {
         if (p.b_e4m3) return false;  // bf16 activations: e5m2 weights only, as on the other small-M routes
         if (p.out_bf16) FEATHER_M16_LAUNCH(true, false, true);
@@ -510,8 +526,8 @@ bool launch_smallm_kernel(const MmArgs& p, void* workspace, size_t workspace_byt
     const bool wide = pl.ct >= 2;
     // A through LDS needs every byte offset into A to fit the copy's 32-bit lane offset
     const bool lds_a = p.M * p.K * 2 < (int64_t(1) << 32);
-    if (mt == 1 && ks == 1 && !wide && lds_a && p.K % 64 == 0 && p.N % 16 == 0 && !m16_disabled())
-        return launch_m16(p, stream);
+    if (mt <= 2 && ks == 1 && !wide && lds_a && p.K % 64 == 0 && p.N % 16 == 0 && !m16_disabled())
+        return mt == 1 ? launch_m16<1>(p, stream) : launch_m16<2>(p, stream);
     switch (mt) {
         case 1:
             if (lds_a) return wide ? launch_mt<1, 4, true>(p, ks, partials, counters, stream)

@@ -550,16 +550,16 @@ def _lean_call(ad, bd, sd, bsd, M, N, K, a_bf16, b_e4m3, out_dtype, has_scale=1,
     return c
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 9, 16])
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 16, 17, 24, 31, 32])
 @pytest.mark.parametrize("variant", ["f16_e5m2_f16", "f16_e4m3_bf16", "bf16_e5m2_f16", "bf16_e5m2_bf16",
                                      "noscale_nobias"])
 def test_small_m_lean_route(cuda, M, variant):
-    """M <= 16 with K % 64 == 0 and one K range per 16-column strip runs the lean small-M
-    kernel, which copies only the A rows below M into LDS: rows >= M of its LDS slabs hold
-    whatever the previous workgroup on that CU left there. A call with M = 16 and an all-NaN
-    A runs first on the same shape, so every slab row past M holds NaN bits when the M-row
-    call runs; its output must still equal the oracle (an output row reads only its own A
-    row) and carry no NaN."""
+    """M <= 32 with K % 64 == 0 and one K range per 16-column strip runs the lean small-M
+    kernel (one or two 16-row tiles), which copies only the A rows below M into LDS: rows >= M
+    of its LDS slabs hold whatever the previous workgroup on that CU left there. A call with
+    M = 16 or 32 and an all-NaN A runs first on the same shape, so every slab row past M holds
+    NaN bits when the M-row call runs; its output must still equal the oracle (an output row
+    reads only its own A row) and carry no NaN."""
     N, K = 4096, 2048
     a_bf16 = variant.startswith("bf16")
     b_e4m3 = "e4m3" in variant
@@ -583,8 +583,9 @@ def test_small_m_lean_route(cuda, M, variant):
     sd = torch.tensor([s], device=cuda)
     bsd = bias.to(cuda)
     # fill the LDS slabs with NaN rows: an M = 16 call on an all-NaN A of the same dtype
-    poison = torch.full((16, K), float("nan"), dtype=a_t.dtype, device=cuda)
-    yp = _lean_call(poison, bd, sd, bsd, 16, N, K, a_bf16, b_e4m3, out_dtype)
+    Mp = 16 if M <= 16 else 32
+    poison = torch.full((Mp, K), float("nan"), dtype=a_t.dtype, device=cuda)
+    yp = _lean_call(poison, bd, sd, bsd, Mp, N, K, a_bf16, b_e4m3, out_dtype)
     assert torch.isnan(yp).all()
     y = _lean_call(a_t.to(cuda), bd, sd, bsd, M, N, K, a_bf16, b_e4m3, out_dtype, has_scale, has_bias)
     od = O.DT_F16 if out_dtype == torch.float16 else O.DT_BF16
