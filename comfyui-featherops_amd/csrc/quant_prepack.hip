@@ -15,8 +15,8 @@
 // c10 conversion: round to nearest even, |x| >= 61440 -> +-inf, NaN -> 0x7f
 // with the sign bit kept.
 //
-// Three kernels: a grid-stride amax that writes one partial maximum per
-// workgroup, a one-workgroup reduction of those partials into one 32-bit
+// Three kernels: an amax over equal contiguous shares of the weight that
+// writes one partial maximum per workgroup, a one-workgroup reduction of those partials into one 32-bit
 // word, then a streaming quantize that recomputes the scale from that word in
 // every thread and writes the prepacked bytes directly (16 output bytes per
 // thread, 1 KB contiguous per wave). The amax pass reads the weight with
@@ -173,12 +173,17 @@ __global__ __launch_bounds__(kAmaxThreads) void amax_kernel(const void* __restri
     const uint4* v16 = static_cast<const uint4*>(w);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     if (!per_element) {
-        // native-bit maximum, four 16-byte loads in flight per thread (also in
-        // the last, partial round: a zero word leaves the maximum unchanged)
-        for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += 4 * stride) {
+        // native-bit maximum over this workgroup's contiguous, equal share of
+        // the vectors, four 16-byte loads in flight per thread (also in the
+        // last, partial round: a zero word leaves the maximum unchanged)
+        const int64_t share = (nvec + gridDim.x - 1) / gridDim.x;
+        const int64_t beg = static_cast<int64_t>(blockIdx.x) * share;
+        const int64_t end = beg + share < nvec ? beg + share : nvec;
+        for (int64_t i = beg + threadIdx.x; i < end; i += 4 * kAmaxThreads) {
             uint4 t[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) t[u] = i + u * stride < nvec ? v16[i + u * stride] : make_uint4(0u, 0u, 0u, 0u);
+            for (int u = 0; u < 4; ++u)
+                t[u] = i + u * kAmaxThreads < end ? v16[i + u * kAmaxThreads] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
             for (int u = 0; u < 4; ++u) m = abs_max_words<DT>(t[u], m);
         }
