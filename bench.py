@@ -2,7 +2,7 @@
 """Headline benchmark: fp16 x fp8-e5m2 scaled_mm on one MI355X.
 
 One step = one launch of the scaled_mm hot path (torch.ops.feather_ops.scaled_mm,
-i.e. launch_scaled_mm of libfeatherops_amd.so) on the BASELINE headline shape
+i.e. launch_scaled_mm of libfeatherops_amd.so) on the headline shape
 M=32768, K=5120, N=13824 (config 4, video-DiT FFN up-projection), fp16 out,
 per-tensor scale and bias, inputs resident in HBM. The weight is a synthetic
 ~N(0, 0.02) fp16 matrix quantized and prepacked on the device by the
@@ -12,12 +12,18 @@ Also measured in the same run (extra keys of the JSON line):
   bf16_activations  the headline shape with bf16 activations through the
               any-M op, beside fp16 activations and torch's cast + the GEMM
   small_m     config 2 (M=16, K=N=4096): GB/s, rotating over enough distinct
-              weights (> 256 MB) that the Infinity Cache cannot serve them
+              weights (> 256 MB) that the Infinity Cache cannot serve them;
+              torch graph replay, plus back-to-back and HIP-graph launches
+              through the C ABI beside a streaming floor timed both ways
   quantize    quantize+prepack of a 13824x5120 fp16 weight (config 5's op),
               four weights in rotation so they stream from HBM
+  hbm_aux     the bf16 -> fp16 casts (N x N, N = 1024 .. 16384) and the
+              dequantize of a 13824x5120 weight, as GB/s
+  reference_published_shape  8192^3 on the reference's published config
+              tuple and on the 256x256 tile (context only)
   lora        an unmerged rank-64 LoRA layer on the headline shape, fused
               epilogue against the reference's separate pass
-  configs     every BASELINE config at one GPU: C1 (M=256, K=N=1024), C3
+  configs     every benchmark workload at one GPU: C1 (M=256, K=N=1024), C3
               (image-DiT linears, M=4096, bf16 out), C4 (video-DiT linears,
               M=32768), C5 (40-block x 6-linear stack at M=32768: on-device
               quantize+prepack of all 240 weights, then the 240 GEMMs); each
@@ -322,7 +328,7 @@ def _gemm_shape(dev, op, quant, g, M, N, K, out_dtype, seed, reps=10):
 
 
 def bench_configs(dev, op, quant, g):
-    """Every BASELINE config on this GPU (see the module docstring)."""
+    """Every benchmark workload on this GPU (see the module docstring)."""
     import torch
 
     out = {}
@@ -551,7 +557,7 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic (A ~ N(0,1) fp16; W ~ N(0,0.02) fp16 quantized+prepacked on device to e5m2)",
         "config": {"workload": "scaled_mm fp16 x e5m2, M32768 K5120 N13824, fp16 out, scale+bias "
-                               "(BASELINE config 4 headline)",
+                               "(the C4 video-DiT up-projection, the headline)",
                    "M": M, "N": N, "K": K, "out_dtype": "fp16", "kernel_config": list(HEADLINE_CFG)},
         "pct_fp16_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",

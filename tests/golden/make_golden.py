@@ -8,7 +8,7 @@ are the committed known answers the GPU tests compare against:
   e5m2_codes.npz    fp8 e5m2 code of every fp16 and every bf16 bit pattern
                     (torch's float -> float8_e5m2 cast, equal to the oracle)
   bf16_rtz.npz      fp16 bits of every bf16 pattern under round-toward-zero
-  quant_c1.npz      BASELINE config 1 weight (N=K=1024, ~N(0, 0.02), seed 0)
+  quant_c1.npz      the C1 workload's weight (N=K=1024, ~N(0, 0.02), seed 0)
                     quantized on the load path (fp32) and the patch path
                     (fp16 with the reciprocal clamp, bf16): sha256 of the
                     prepacked bytes, the scale, 32 sampled rows

@@ -1,4 +1,4 @@
-"""BASELINE config 5 end to end on the device: the 40-block DiT linear stack at hidden size 5120,
+"""The C5 workload end to end on the device: the 40-block DiT linear stack at hidden size 5120,
 FFN 13824, M = 32768. Every one of the 240 weights is quantized and prepacked on the device by
 the load path (comfy_feather/quant.py:116-136 of the reference) and checked bit for bit against
 torch's e5m2 cast of the same fp32 product (the cast the oracle's encoder is pinned to); every

@@ -461,7 +461,7 @@ def test_every_fp8_code_decodes_exactly(cuda, b_dtype, route):
 
 
 def test_baseline_config1_gemm(cuda, hk, quant):
-    """BASELINE config 1 end to end: A (256,1024) ~N(0,1) fp16, W (1024,1024) ~N(0,0.02) in fp16
+    """The C1 workload (the reference's CPU-runnable case) end to end: A (256,1024) ~N(0,1) fp16, W (1024,1024) ~N(0,0.02) in fp16
     quantized on the load path (its bytes and scale equal the golden fixture), fp16 out with a
     bias; the GEMM through the C ABI on every config tuple that takes M=256, through the
     reference's torch op and through the drop-in Python entries, each against the oracle over
@@ -499,7 +499,7 @@ def test_baseline_config1_gemm(cuda, hk, quant):
     assert_gemm_close(y, ref, torch.float16, "C1 scaled_mm_hip", literal=True)
     y = hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16)
     assert_gemm_close(y, ref, torch.float16, "C1 any-M", literal=True)
-    # the route BASELINE config 1 takes by default (the 64x64 split-K-route tiles, unsplit at K=1024) is deterministic
+    # the route the C1 workload takes by default (the 64x64 split-K-route tiles, unsplit at K=1024) is deterministic
     assert torch.equal(y, hk.scaled_mm_hip_any_m(ad, bp, sd, bsd, torch.float16))
 
 
