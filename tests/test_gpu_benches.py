@@ -41,3 +41,29 @@ def test_config_sweep_script():
     assert any(ln.strip().startswith("any_m pick=") for ln in lines)
     for ln in lines:
         assert float(re.search(r"avg_TFLOPS=([0-9.]+)", ln).group(1)) > 0
+
+
+@pytest.mark.parametrize("args,title", [
+    (["--convert", "rtz", "--n", 1024, "--rotate", 4], "bf16_to_fp16 benchmark"),
+    (["--convert", "rne", "--n", 2048, "--rotate", 2], "bf16_to_fp16_rne benchmark"),
+    (["--dequant", "--n", 1024, "--k", 2048, "--rotate", 2], "dequantize_e5m2 benchmark"),
+    (["--quant", "--n", 1024, "--k", 2048, "--rotate", 2], "quantize_prepack_e5m2 benchmark"),
+    (["--m", 16, "--n", 1024, "--k", 1024, "--rotate", 4, "--warps_m", 1, "--warps_n", 1, "--unroll", 2,
+      "--repeat_m", 1, "--repeat_n", 2], "scaled_mm benchmark"),
+])
+def test_cpp_bench_modes(args, title):
+    """The C++ bench's auxiliary modes (the casts and the dequantize, the quantize) and the GEMM's
+    back-to-back and HIP-graph replay timings run and report a positive rate."""
+    exe = PKG / "cpp_benchmarks" / "build" / "benchmark_scaled_mm_hip"
+    text = _run([exe, *args, "--warmup", 2, "--iters", 8])
+    assert title in text, text
+    assert re.search(r"back-to-back (us|ms): [0-9.]*[1-9]", text), text
+    if title == "scaled_mm benchmark":
+        assert re.search(r"graph-replay us: [0-9.]*[1-9]", text), text
+
+
+def test_hbm_copy_floor_both_launch_methods():
+    exe = PKG / "cpp_benchmarks" / "build" / "benchmark_hbm_copy"
+    plain = _run([exe, "--read-bytes", 4 << 20])
+    graph = _run([exe, "--read-bytes", 4 << 20, "--graph"])
+    assert re.search(r"us/call", plain) and "(graph replay)" in graph
