@@ -354,25 +354,28 @@ template <bool kRne, bool kNT>
 __global__ __launch_bounds__(256) void bf16_to_fp16_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                                            int64_t n) {
     const int64_t nvec = n / 8;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     const uint4* in4 = reinterpret_cast<const uint4*>(in);
     uint4* out4 = reinterpret_cast<uint4*>(out);
     auto cvt = [](uint4 t) {
         return make_uint4(bf16x2_to_fp16x2<kRne>(t.x), bf16x2_to_fp16x2<kRne>(t.y), bf16x2_to_fp16x2<kRne>(t.z),
                           bf16x2_to_fp16x2<kRne>(t.w));
     };
-    // four 16-byte loads in flight per thread, also in the last, partial round
-    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < nvec; g += 4 * stride) {
+    // each workgroup streams a contiguous, equal share of the vectors (16 KB
+    // per round: four 16-byte loads in flight per thread, also in the last,
+    // partial round)
+    const int64_t share = (nvec + gridDim.x - 1) / gridDim.x;
+    const int64_t beg = static_cast<int64_t>(blockIdx.x) * share;
+    const int64_t end = beg + share < nvec ? beg + share : nvec;
+    for (int64_t g = beg + threadIdx.x; g < end; g += 4 * 256) {
         uint4 t[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            t[u] = g + u * stride < nvec ? (kNT ? ld_nt16(&in4[g + u * stride]) : in4[g + u * stride])
-                                         : make_uint4(0u, 0u, 0u, 0u);
+            t[u] = g + u * 256 < end ? (kNT ? ld_nt16(&in4[g + u * 256]) : in4[g + u * 256]) : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            if (g + u * stride < nvec) {
-                if (kNT) st_nt16(&out4[g + u * stride], cvt(t[u]));
-                else out4[g + u * stride] = cvt(t[u]);
+            if (g + u * 256 < end) {
+                if (kNT) st_nt16(&out4[g + u * 256], cvt(t[u]));
+                else out4[g + u * 256] = cvt(t[u]);
             }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
