@@ -592,3 +592,27 @@ def test_small_m_lean_route(cuda, M, variant):
     ref = O.scaled_mm_ref(a_t.to(torch.float16).numpy(), packed, s if has_scale else None,
                           bias_np if has_bias else None, od, "e4m3fn" if b_e4m3 else "e5m2")
     assert_gemm_close(y, ref, out_dtype, f"lean {variant} M={M}")
+
+
+@pytest.mark.parametrize("M", [5, 16, 20, 32])
+@pytest.mark.parametrize("N,K", [(1040, 64), (2048, 1088), (1024, 4160), (4096, 64 * 129)])
+def test_small_m_lean_stage_counts(cuda, M, N, K):
+    """The lean small-M kernel over stage counts that do not fill its rounds (one 64-K stage; 17,
+    65 and 129 stages against 16 waves x 4 or 2 stages per round) and N a multiple of 16 only:
+    whole output against the oracle, through the workspace entry (same route as the torch op)."""
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    a = torch.randn(M, K, generator=g).half()
+    packed, s = weight_like(N, K, g)
+    bias, bias_np = _bias_for(torch.float16, N, g)
+    cfg = (1, 1, 2, 1, 2)
+    nbytes = lib().feather_scaled_mm_workspace_size(M, N, K, *cfg)
+    ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=cuda)
+    ad, bd, sd, bsd = a.to(cuda), to_dev_codes(packed, cuda), torch.tensor([s], device=cuda), bias.to(cuda)
+    c = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
+    print("lean stages", M, N, K, flush=True)
+    assert lib().feather_launch_scaled_mm_ws(ad.data_ptr(), bd.data_ptr(), sd.data_ptr(), bsd.data_ptr(),
+                                             c.data_ptr(), M, N, K, 1, 1, *cfg, 1, 0, ws.data_ptr(), ws.numel(),
+                                             stream(cuda))
+    torch.cuda.synchronize()
+    ref = O.scaled_mm_ref(a.numpy(), packed, s, bias_np, O.DT_F16)
+    assert_gemm_close(c, ref, torch.float16, f"lean {M}x{N}x{K}")
