@@ -430,25 +430,42 @@ struct SmallmPlan {
     int ks;  // workgroups per strip (K split)
 };
 
-// Cost model for M <= 32, in microseconds, fitted to MI355X runs over
-// M = 1..32, N = 3072..13824, K = 3072..13824 with rotated weights. A
-// workgroup holds 128 KB of LDS, so one runs per CU and a grid larger than
-// the CU count runs in rounds. Each wave keeps a fixed number of 16-byte
-// weight loads in flight, so a workgroup's rate is bounded by its bytes in
-// flight over the loaded HBM latency: a 16-column strip (one load per stage
-// per wave) streams 1 KB of weight per ~0.052 us, a 64-column strip (twice
-// the loads in flight) per ~0.027 us. On top of that: ~3.1 us per round
-// (launch, first-load latency, reduction and epilogue), a whole-chip ceiling
-// of ~7 TB/s, and ~2.6 us for a K split across workgroups (partials out,
-// arrival counter, last-arriver sum).
-double smallm_cost_us(int64_t N, int64_t nst, int ct, int ks, int cus) {
+// Cost model for M <= 32, in microseconds, from MI355X runs with rotated
+// weights. A workgroup holds 128 KB of LDS, so one runs per CU and a grid
+// larger than the CU count runs in rounds; each wave keeps a fixed number of
+// 16-byte weight loads in flight, so a workgroup streams at a rate bounded by
+// its bytes in flight over the loaded HBM latency. For one row tile (M <= 16)
+// the terms are fitted per kernel: a fixed cost, a cost per round (launch,
+// first-load latency, reduction, epilogue; a K split adds its partials and
+// arrival counter here), a cost per KB one CU streams that grows with the rows
+// of A (the A copies and MFMA issue of a stage), and a cost per MB of weight
+// (the whole-chip share). For two row tiles: a 16-column strip streams 1 KB of
+// weight per ~0.052 us, a 64-column strip (twice the loads in flight) per
+// ~0.027 us, ~3.1 us per round, a whole-chip ceiling of ~7 TB/s, and ~2.6 us
+// for a K split across workgroups.
+double smallm_cost_us(int64_t M, int64_t N, int64_t nst, int ct, int ks, int cus) {
     const int64_t nstrips = (N + 16 * ct - 1) / (16 * ct);
     const int64_t groups = nstrips * ks;
     const int64_t rounds = (groups + cus - 1) / cus;
     const double kb_per_group = static_cast<double>(ct) * static_cast<double>((nst + ks - 1) / ks);
+    const double work = static_cast<double>(rounds) * kb_per_group;  // KB one CU streams
+    const double mb = static_cast<double>(nst) * static_cast<double>(N) * 1024.0 / 16.0 / 1.0e6;  // MB of weight
+    if (M <= 16) {
+        // one row tile: least-squares fits of measured back-to-back times
+        // (M = 1..16, N = 2048..13824, K = 5120..16384), one per kernel: the
+        // lean kernel (16-column strips, no split), the general kernel with
+        // 16-column strips split over K, and 64-column strips split over K
+        struct Fit { double c0, round, kb, kb_row, mb; };
+        constexpr Fit kLean{0.05, 1.80, 0.0213, 0.0012, 0.086};
+        constexpr Fit kStripSplit{1.51, 2.70, 0.0184, 0.0009, 0.122};
+        constexpr Fit kWideSplit{2.57, 2.99, 0.0108, 0.0003, 0.116};
+        const Fit& f = ct >= 4 ? kWideSplit : ks > 1 ? kStripSplit : kLean;
+        return f.c0 + f.round * static_cast<double>(rounds) + (f.kb + f.kb_row * static_cast<double>(M)) * work +
+               f.mb * mb;
+    }
     const double per_kb = ct >= 4 ? 0.027 : 0.052;
     const double t_rounds = static_cast<double>(rounds) * (3.1 + kb_per_group * per_kb);
-    const double t_chip = 3.1 + static_cast<double>(nst) * static_cast<double>(N) * 1024.0 / 16.0 / 7.0e6;
+    const double t_chip = 3.1 + mb / 7.0;
     return (t_rounds > t_chip ? t_rounds : t_chip) + (ks > 1 ? 2.6 : 0.0);
 }
 
@@ -470,10 +487,10 @@ SmallmPlan smallm_plan(int64_t M, int64_t N, int64_t K, int target_groups, bool 
         if (ks > max_ks) ks = max_ks;
         pl = ks > 1 ? SmallmPlan{pl.ct, static_cast<int>(ks)} : SmallmPlan{1, 1};
     } else {
-        double best = smallm_cost_us(N, nst, 1, 1, cus);
+        double best = smallm_cost_us(M, N, nst, 1, 1, cus);
         for (int ct : {1, 4})
             for (int ks = 1; ks <= max_ks; ++ks) {
-                const double c = smallm_cost_us(N, nst, ct, ks, cus);
+                const double c = smallm_cost_us(M, N, nst, ct, ks, cus);
                 if (c < best) {
                     best = c;
                     pl = SmallmPlan{ct, ks};

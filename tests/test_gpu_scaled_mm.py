@@ -244,7 +244,7 @@ def test_baseline_config4_video_dit(cuda, K, N):
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (16, 3072, 3072), (1, 1040, 2048), (33, 2000, 4096),
                                    (64, 4096, 4096), (48, 12288, 2048), (16, 128, 128), (16, 5120, 13824),
-                                   (1, 3072, 12288), (32, 5120, 13824), (7, 2000, 8192)])
+                                   (1, 3072, 12288), (8, 2048, 12288), (32, 5120, 13824), (7, 2000, 8192)])
 def test_small_m_split_k_workspace(cuda, M, N, K):
     """feather_launch_scaled_mm_ws: K split across workgroups through the
     workspace; twice in a row (the arrival counters must come back to zero)."""
@@ -285,7 +285,7 @@ def test_workspace_shared_across_shapes(cuda):
     split-K LDS tiles, each shape twice, fewer tiles before more."""
     from gpu_util import lib, stream
 
-    seq = [(16, 3072, 12288), (16, 5120, 13824), (1, 3072, 12288), (256, 1024, 2112), (512, 1072, 2048),
+    seq = [(16, 3072, 12288), (16, 5120, 13824), (8, 2048, 12288), (256, 1024, 2112), (512, 1072, 2048),
            (64, 4096, 4096), (48, 12288, 2048), (16, 5120, 13824), (512, 1072, 2048)]
     cfg = (2, 2, 4, 4, 4)
     need = max(lib().feather_scaled_mm_workspace_size(M, N, K, *cfg) for M, N, K in seq)

@@ -238,7 +238,9 @@ def test_small_m_plan_workspace(pkg):
     assert lib.feather_scaled_mm_workspace_size(16, 13824, 5120, *cfg) == 0  # 216 strips of 64 columns
     # 80 strips of 64 columns x 3 K ranges: the fixed 64 KB counter region + 3 fp32 partial tiles per strip
     assert lib.feather_scaled_mm_workspace_size(16, 5120, 13824, *cfg) == 65536 + 80 * 3 * 16 * 64 * 4
-    assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 65536 + 48 * 4 * 1 * 64 * 4
+    assert lib.feather_scaled_mm_workspace_size(1, 3072, 12288, *cfg) == 0  # lean kernel: 192 strips of 16 columns
+    # 128 strips of 16 columns x 2 K ranges
+    assert lib.feather_scaled_mm_workspace_size(8, 2048, 12288, *cfg) == 65536 + 128 * 2 * 8 * 16 * 4
 
 
 def test_packed_params_protocol(quant):

@@ -47,12 +47,12 @@ def _run_noalloc(a, bd, sd, bias, M, N, K, cfg, a_code):
 
 SEQUENCES = [
     # small-M kernel with a K split across workgroups, then a smaller one
-    [(16, 5120, 13824, (1, 1, 2, 1, 2)), (1, 3072, 12288, (1, 1, 2, 1, 2))],
+    [(16, 5120, 13824, (1, 1, 2, 1, 2)), (8, 2048, 12288, (1, 1, 2, 1, 2))],
     # split-K LDS tiles (64 x 64 and 32 x 128), then smaller
     [(64, 4096, 4096, (2, 2, 4, 4, 4)), (48, 1024, 1024, (2, 2, 4, 4, 4))],
     [(256, 3072, 3072, (2, 2, 4, 4, 4)), (128, 1024, 1024, (2, 2, 4, 4, 4))],
     # no split needed (large tiles), then a split-K shape
-    [(512, 2048, 1024, (2, 4, 4, 8, 4)), (16, 2048, 4096, (1, 1, 2, 1, 2))],
+    [(512, 2048, 1024, (2, 4, 4, 8, 4)), (16, 2048, 12288, (1, 1, 2, 1, 2))],
 ]
 
 
