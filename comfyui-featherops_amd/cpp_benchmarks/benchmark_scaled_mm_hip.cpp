@@ -12,9 +12,13 @@
 // buffers so that a weight larger than the 256 MB Infinity Cache in total is
 // streamed from HBM), --b e5m2|e4m3. Default config is the gfx950 256x256
 // tile (2,4,4,8,4).
-// --quant: time feather_quantize_prepack_e5m2 on an N x K fp16 weight instead
-// (amax pass + quantize/prepack pass, 5 bytes per element of algorithmic
-// traffic: 2 read for the amax, 2 read + 1 written for the codes).
+// --quant: time feather_quantize_prepack_e5m2_ws (the torch op's entry) on an
+// N x K fp16 weight instead: one pass (3 bytes per element: the weight read
+// once, the codes written) where the weight fits the registers of the chip,
+// else an amax pass + a quantize/prepack pass (5 bytes per element: 2 read for
+// the amax, 2 read + 1 written for the codes); rates are printed for both byte
+// counts. --quant-two-pass: the same through feather_quantize_prepack_e5m2,
+// always two passes.
 // --lora-down R: time feather_lora_down instead, T (M x R) = x (M x K) . D^T
 // with bf16 x ~ U[-1, 1) rotated over --rotate buffers and D (R x K), GB/s on
 // the bytes of x, D and T.
@@ -60,6 +64,7 @@ struct Opts {
     int b_dtype = FEATHER_B_E5M2;
     int rotate = 1;
     bool quant = false;
+    bool quant_two_pass = false;
     int64_t lora_rank = 0;
     int convert = 0;  // 1 rtz, 2 rne
     bool dequant = false;
@@ -68,7 +73,7 @@ struct Opts {
 void usage(const char* argv0) {
     std::cout << "Usage: " << argv0
               << " [--m M] [--n N] [--k K] [--warmup W] [--iters I] [--warps_m M] [--warps_n N] [--unroll U]"
-                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant]"
+                 " [--repeat_m RM] [--repeat_n RN] [--out fp16|bf16] [--b e5m2|e4m3] [--rotate R] [--quant] [--quant-two-pass]"
                  " [--lora-down R] [--convert rtz|rne] [--dequant]\n";
 }
 
@@ -97,6 +102,7 @@ Opts parse(int argc, char** argv) {
         else if (a == "--b") o.b_dtype = val() == "e4m3" ? FEATHER_B_E4M3FN : FEATHER_B_E5M2;
         else if (a == "--rotate") o.rotate = std::max(1, std::stoi(val()));
         else if (a == "--quant") o.quant = true;
+        else if (a == "--quant-two-pass") o.quant = o.quant_two_pass = true;
         else if (a == "--lora-down") o.lora_rank = std::stoll(val());
         else if (a == "--convert") o.convert = val() == "rne" ? 2 : 1;
         else if (a == "--dequant") o.dequant = true;
@@ -138,18 +144,23 @@ int run_quant(const Opts& o) {
     }
     uint8_t* dq;
     float* dscale;
-    uint32_t* dws;
+    void* dws;
+    const size_t ws_bytes = feather_quantize_workspace_size();
     HIP_OK(hipMalloc(&dq, nw));
     HIP_OK(hipMalloc(&dscale, sizeof(float)));
-    HIP_OK(hipMalloc(&dws, 1024));
+    HIP_OK(hipMalloc(&dws, ws_bytes));
+    HIP_OK(hipMemset(dws, 0, ws_bytes));  // the _ws entry's counters start at zero
     hipStream_t stream;
     hipEvent_t t0, t1;
     HIP_OK(hipStreamCreate(&stream));
     HIP_OK(hipEventCreate(&t0));
     HIP_OK(hipEventCreate(&t1));
     auto run = [&](int i) {
-        const int rc = feather_quantize_prepack_e5m2(dw[i % o.rotate], FEATHER_DTYPE_F16, o.n, o.k, nullptr, 0, dq,
-                                                     dscale, dws, stream);
+        const int rc = o.quant_two_pass
+                           ? feather_quantize_prepack_e5m2(dw[i % o.rotate], FEATHER_DTYPE_F16, o.n, o.k, nullptr, 0,
+                                                           dq, dscale, static_cast<uint32_t*>(dws), stream)
+                           : feather_quantize_prepack_e5m2_ws(dw[i % o.rotate], FEATHER_DTYPE_F16, o.n, o.k, nullptr,
+                                                              0, dq, dscale, dws, ws_bytes, stream);
         if (rc != FEATHER_OK) {
             std::cerr << "quantize failed: " << feather_status_string(rc) << std::endl;
             std::exit(1);
@@ -167,7 +178,9 @@ int run_quant(const Opts& o) {
     const double bytes = 5.0 * static_cast<double>(nw);
     std::cout << std::fixed << std::setprecision(4);
     std::cout << "quantize_prepack_e5m2 benchmark\n  problem: n=" << o.n << " k=" << o.k << " fp16 rotate=" << o.rotate
-              << "\n  back-to-back ms: " << ms << "  (GB/s " << bytes / ms / 1e6 << " on 5 B/element)" << std::endl;
+              << (o.quant_two_pass ? " two-pass entry" : "") << "\n  back-to-back ms: " << ms << "  (GB/s "
+              << bytes / ms / 1e6 << " on 5 B/element, " << 0.6 * bytes / ms / 1e6
+              << " on 3 B/element: the weight read once, the codes written once)" << std::endl;
     for (auto p : dw) HIP_OK(hipFree(p));
     HIP_OK(hipFree(dq));
     HIP_OK(hipFree(dscale));

@@ -332,6 +332,36 @@ int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t
     return launch_status();
 }
 
+size_t feather_quantize_workspace_size(void) { return feather::kWorkspaceCounterBytes + 4096; }
+
+int feather_quantize_prepack_e5m2_ws(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,
+                                     int native, uint8_t* out, float* scale_out, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+    if (!workspace || workspace_bytes < feather_quantize_workspace_size()) return FEATHER_ERR_INVALID;
+    if (!w || !out || !scale_out) return FEATHER_ERR_INVALID;
+    if (w_dtype != FEATHER_DTYPE_F16 && w_dtype != FEATHER_DTYPE_BF16 && w_dtype != FEATHER_DTYPE_F32)
+        return FEATHER_ERR_INVALID;
+    if (N <= 0 || K <= 0 || K % 16 != 0 || N > INT32_MAX || K > INT32_MAX || (N + 63) / 64 > 65535)
+        return FEATHER_ERR_INVALID;
+    if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u)) return FEATHER_ERR_INVALID;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    feather::QuantArgs q;
+    q.w = w;
+    q.dtype = w_dtype;
+    q.N = N;
+    q.K = K;
+    q.ckpt_scale = ckpt_scale;
+    q.native = native != 0;
+    q.out = out;
+    q.scale_out = scale_out;
+    q.workspace = reinterpret_cast<uint32_t*>(ws + feather::kWorkspaceCounterBytes);  // partial maxima
+    q.scale_in = nullptr;
+    q.counters = reinterpret_cast<uint32_t*>(ws);  // two words of the zero region
+    q.cus = device_cus() <= 1024 ? device_cus() : 0;
+    feather::launch_quantize_prepack(q, stream);
+    return launch_status();
+}
+
 int feather_quantize_prepack_e5m2_scaled(const void* w, int w_dtype, int64_t N, int64_t K, const float* scale,
                                          uint8_t* out, hipStream_t stream) {
     if (!w || !out || !scale) return FEATHER_ERR_INVALID;

@@ -19,6 +19,10 @@ struct QuantArgs {
     float* scale_out;         // device scalar
     uint32_t* workspace;      // >= 1024 bytes of device memory: partial maxima (unused when scale_in is set)
     const float* scale_in;    // device scalar: use this scale instead of recalculating (native only)
+    // two device words, zero on entry and left zero, for the one-pass kernel's
+    // grid barrier (null: two passes); the partials then need 4 bytes per CU
+    uint32_t* counters = nullptr;
+    int cus = 0;              // compute units of the device (one-pass grid)
 };
 
 void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream);

@@ -26,6 +26,8 @@
 // with 13824 x 5120 fp16 weights rotated through 566 MB: 74 -> 68 us per
 // weight; nontemporal amax loads as well make it 80 us (the quantize pass then
 // finds nothing resident).
+#include <cstdlib>
+
 #include "feather_common.h"
 #include "quant_prepack.h"
 
@@ -44,23 +46,26 @@ __device__ __forceinline__ void st_nt16(void* p, uint4 v) {
 constexpr float kE5m2Max = 57344.0f;
 constexpr float kFp16Max = 65504.0f;
 
-// fp32 -> fp8 e5m2, round to nearest even, |x| >= 61440 -> inf.
-__device__ __forceinline__ uint32_t f32_to_e5m2(float f) {
-    const uint32_t u = f32_bits(f);
-    const uint32_t sign = (u >> 24) & 0x80u;
-    const uint32_t a = u & 0x7fffffffu;
-    uint32_t r;
-    if (a > 0x7f800000u) {
-        r = 0x7fu;                          // NaN
-    } else if (a >= 0x47700000u) {          // 61440.0f: ties to even go up to 2^16 = inf
-        r = 0x7cu;
-    } else if (a >= 0x38800000u) {          // >= 2^-14: normal e5m2
-        const uint32_t lsb = (a >> 21) & 1u;
-        r = ((a + 0x000fffffu + lsb) >> 21) - (112u << 2);  // re-bias exponent 127 -> 15
-    } else {                                // subnormal: multiples of 2^-16, exact scaling, RNE
-        r = static_cast<uint32_t>(__builtin_rintf(bits_f32(a) * 65536.0f));
+// Four fp32 -> fp8 e5m2 codes, a in the low byte: torch's c10 conversion,
+// round to nearest even, |x| >= 61440 -> +-inf, NaN -> 0x7f with the sign bit
+// kept. The hardware conversion (v_cvt_pk_bf8_f32, OCP e5m2, no clamp) gives
+// exactly these codes for every non-NaN fp32 input (all 2^32 bit patterns
+// compared on MI355X against a bit-level restatement of the rule above) and
+// another NaN code, so NaN inputs are patched afterwards (kNan; callers leave
+// it out where no input can be NaN).
+template <bool kNan>
+__device__ __forceinline__ uint32_t f32x4_to_e5m2(float a, float b, float c, float d) {
+    uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
+    w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, static_cast<int>(w), true));
+    if constexpr (kNan) {
+        const float v[4] = {a, b, c, d};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (__builtin_isnan(v[k]))
+                w = (w & ~(0xffu << (8 * k))) | ((0x7fu | ((f32_bits(v[k]) >> 24) & 0x80u)) << (8 * k));
+        }
     }
-    return r | sign;
+    return w;
 }
 
 template <int DT>
@@ -81,6 +86,24 @@ struct WeightType<kDtypeF32> {
     __device__ static float round(float f) { return f; }
 };
 
+// 16 fp16 / bf16 elements held as two 16-byte words -> fp32 (exact).
+template <int DT>
+__device__ __forceinline__ void decode16(const uint4 (&r)[2], float (&v)[16]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const uint16_t lo = static_cast<uint16_t>(w[h] & 0xffffu), hi = static_cast<uint16_t>(w[h] >> 16);
+            if constexpr (DT == kDtypeF16) {
+                v[8 * j + 2 * h] = half_bits_to_f32(lo); v[8 * j + 2 * h + 1] = half_bits_to_f32(hi);
+            } else {
+                v[8 * j + 2 * h] = bf16_bits_to_f32(lo); v[8 * j + 2 * h + 1] = bf16_bits_to_f32(hi);
+            }
+        }
+    }
+}
+
 // 16 consecutive elements starting at element index i (16-byte aligned).
 template <int DT>
 __device__ __forceinline__ void load16(const void* p, int64_t i, float (&v)[16]) {
@@ -94,20 +117,8 @@ __device__ __forceinline__ void load16(const void* p, int64_t i, float (&v)[16])
         }
     } else {
         const uint4* q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint4 t = ld_nt16(&q[j]);
-            const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const uint16_t lo = static_cast<uint16_t>(w[h] & 0xffffu), hi = static_cast<uint16_t>(w[h] >> 16);
-                if constexpr (DT == kDtypeF16) {
-                    v[8 * j + 2 * h] = half_bits_to_f32(lo); v[8 * j + 2 * h + 1] = half_bits_to_f32(hi);
-                } else {
-                    v[8 * j + 2 * h] = bf16_bits_to_f32(lo); v[8 * j + 2 * h + 1] = bf16_bits_to_f32(hi);
-                }
-            }
-        }
+        const uint4 r[2] = {ld_nt16(&q[0]), ld_nt16(&q[1])};
+        decode16<DT>(r, v);
     }
 }
 
@@ -239,6 +250,80 @@ __global__ __launch_bounds__(kAmaxParts) void amax_finalize_kernel(uint32_t* __r
     }
 }
 
+// How the codes are computed, decided once per kernel from the scale (the
+// same for every thread): the patch path (arithmetic in the weight's dtype)
+// or the load path (fp32 on w * ckpt_scale); on the load path with
+// ckpt_scale == 1 the first multiply is left out (v * 1 == v exactly for the
+// non-NaN v it is used with); NaN codes need patching only when the amax of
+// the products or the reciprocal of the scale is not finite (otherwise every
+// product is a finite number times a finite number: never NaN).
+enum QuantMode : int { kModeLoad = 0, kModeLoadUnit = 1, kModeNative = 2, kModeNan = 4 };
+
+struct QuantScale {
+    float inv;  // T(1/s) on the patch path, 1/s on the load path
+    float cs;   // ckpt_scale (load path), 1 otherwise
+    int mode;
+};
+
+// amax_finite: false when unknown (a caller-given scale)
+template <int DT>
+__device__ __forceinline__ QuantScale quant_scale(float s, bool native, float cs, bool amax_finite) {
+    QuantScale q;
+    q.cs = native ? 1.0f : cs;
+    q.inv = native ? WeightType<DT>::round(1.0f / s) : 1.0f / s;
+    const bool nan = !amax_finite || !(__builtin_fabsf(q.inv) <= 3.402823466e38f);
+    q.mode = native ? kModeNative : (q.cs == 1.0f && !nan ? kModeLoadUnit : kModeLoad);
+    if (nan) q.mode |= kModeNan;
+    return q;
+}
+
+template <int DT, int kMode>
+__device__ __forceinline__ float scaled_elem(float v, float inv, float cs) {
+    if constexpr ((kMode & kModeNative) != 0) return WeightType<DT>::round(opaque_f32(v * inv));
+    else if constexpr ((kMode & kModeLoadUnit) != 0) return v * inv;
+    else return (v * cs) * inv;
+}
+
+template <int DT, int kMode>
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float inv, float cs) {
+    return f32x4_to_e5m2<(kMode & kModeNan) != 0>(scaled_elem<DT, kMode>(a, inv, cs), scaled_elem<DT, kMode>(b, inv, cs),
+                                                 scaled_elem<DT, kMode>(c, inv, cs), scaled_elem<DT, kMode>(d, inv, cs));
+}
+
+// 16 elements -> 16 e5m2 codes
+template <int DT, int kMode>
+__device__ __forceinline__ uint4 quant16(const float (&v)[16], float inv, float cs) {
+    return make_uint4(quant4<DT, kMode>(v[0], v[1], v[2], v[3], inv, cs),
+                      quant4<DT, kMode>(v[4], v[5], v[6], v[7], inv, cs),
+                      quant4<DT, kMode>(v[8], v[9], v[10], v[11], inv, cs),
+                      quant4<DT, kMode>(v[12], v[13], v[14], v[15], inv, cs));
+}
+
+// 8 fp16 / bf16 elements held as one 16-byte word -> 8 codes (fewer live
+// registers where the caller keeps many words resident)
+template <int DT, int kMode>
+__device__ __forceinline__ uint2 quant8(uint4 r, float inv, float cs) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint16_t bits = static_cast<uint16_t>(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu);
+        v[e] = DT == kDtypeF16 ? half_bits_to_f32(bits) : bf16_bits_to_f32(bits);
+    }
+    return make_uint2(quant4<DT, kMode>(v[0], v[1], v[2], v[3], inv, cs),
+                      quant4<DT, kMode>(v[4], v[5], v[6], v[7], inv, cs));
+}
+
+// calls BODY with the kernel's mode as a compile-time constant kM
+#define FEATHER_QUANT_MODES(mode, BODY)                                          \
+    switch (mode) {                                                               \
+        case kModeLoad: { constexpr int kM = kModeLoad; BODY; } break;             \
+        case kModeLoadUnit: { constexpr int kM = kModeLoadUnit; BODY; } break;     \
+        case kModeNative: { constexpr int kM = kModeNative; BODY; } break;         \
+        case kModeLoad | kModeNan: { constexpr int kM = kModeLoad | kModeNan; BODY; } break; \
+        default: { constexpr int kM = kModeNative | kModeNan; BODY; } break;       \
+    }
+
 // grid: (ceil(K/16 / 4), ceil(N / 64)); block 256 = 64 rows (n) x 4 K-groups.
 template <int DT>
 __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restrict__ w, int N, int K,
@@ -247,8 +332,11 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
                                                             const float* __restrict__ scale_in,
                                                             uint8_t* __restrict__ out, float* __restrict__ scale_out) {
     // scale_in: caller-supplied scale (quant.py:59-62), no recalculation and no clamp
-    const float s = scale_in ? scale_in[0] : scale_from_amax<DT>(amax_bits[0], native != 0);
+    const uint32_t amax = scale_in ? 0u : amax_bits[0];
+    const float s = scale_in ? scale_in[0] : scale_from_amax<DT>(amax, native != 0);
     if (scale_out && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) scale_out[0] = s;
+    const QuantScale qs =
+        quant_scale<DT>(s, native != 0, ckpt_scale ? ckpt_scale[0] : 1.0f, !scale_in && amax < 0x7f800000u);
     // thread t takes row n0 + t / 4 and K group i0 + t % 4: a wave's loads
     // cover 16 whole 128-byte row segments (16 cache lines per instruction
     // instead of 64 with one row per lane), and its stores 4 runs of 16
@@ -259,23 +347,216 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
 
     float v[16];
     load16<DT>(w, static_cast<int64_t>(n) * K + i * 16, v);
-    uint32_t q[16];
-    if (native) {
-        const float inv = WeightType<DT>::round(1.0f / s);
+    uint8_t* dst = out + (static_cast<int64_t>(i) * N + n) * 16;
+    FEATHER_QUANT_MODES(qs.mode, st_nt16(dst, quant16<DT, kM>(v, qs.inv, qs.cs)))
+}
+
+// One-pass quantize for fp16 / bf16 weights that fit in the registers of one
+// workgroup per CU (kResRounds blocks of 64 rows x 256 elements per
+// workgroup: 80 MB of bf16 on 256 CUs). Each workgroup loads its blocks once
+// (each wave instruction two whole 512-byte row runs) and keeps them in VGPRs;
+// the workgroups exchange their partial maxima through a grid barrier (every
+// workgroup's partial is stored with a device-coherent store and acknowledged
+// before its arrival is counted; the partials are read only after all
+// arrivals are seen), then quantize from the registers, block by block through
+// LDS, so that each wave stores one K group of 64 consecutive rows (1 KB
+// contiguous in the (K/16, N, 16) layout): 3 bytes of HBM traffic per element
+// instead of the two-pass path's 5.
+//
+// The grid is one workgroup per CU, which a 1024-thread workgroup with this
+// register budget fills, so every workgroup is resident at once on an idle
+// device. The wait is bounded: a workgroup that does not see every arrival
+// within spin_limit polls (for instance when another stream's kernels hold
+// CUs) takes the amax over the whole weight by itself and goes on, so every
+// workgroup finishes in any case, with the same result.
+//
+// Counters (words of a region that is zero on entry and left zero): arrivals
+// and departures are first counted per XCD (workgroup b runs on XCD b % 8),
+// each XCD's count on a line of its own, and the last workgroup of an XCD adds
+// the XCD's total to the global word: 256 same-address atomics in a row would
+// serialise (~10 ns each). The last workgroup to depart (all have then
+// stopped reading) sets every counter back to zero. parts: one word per
+// workgroup, overwritten.
+constexpr int kResThreads = 1024;
+constexpr int kResRounds = 10;
+constexpr int kResXcds = 8;
+constexpr int kResLdsStride = 33;  // 16-byte chunks per LDS row: 32 + 1 pad (conflict-free column reads)
+// counter words: global arrivals, global departures, then per-XCD arrivals and
+// departures 64 words (256 bytes) apart
+__host__ __device__ constexpr int res_arrive_word(int x) { return 64 * (1 + x); }
+__host__ __device__ constexpr int res_depart_word(int x) { return 64 * (1 + kResXcds + x); }
+
+// The store phase of quant_resident_kernel: round j's block goes through LDS
+// (stage[j & 1]; the barrier of round j + 1 orders round j's reads before
+// round j + 2's writes), wave g quantizes K group g of the block for rows
+// tid & 63 and stores them as 1 KB contiguous.
+template <int DT, int kMode>
+__device__ __forceinline__ void resident_store(const uint4 (&raw)[kResRounds][2], uint4 (*stage)[64 * kResLdsStride],
+                                               int beg, int end, int nkb, int kg, int N, const QuantScale& qs,
+                                               uint8_t* __restrict__ out) {
+    const int tid = threadIdx.x;
+    const int lrow = tid >> 5, lcol = tid & 31;
+    const int sg = tid >> 6, srow = tid & 63;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2(WeightType<DT>::round(opaque_f32(v[j] * inv)));
-    } else {
-        const float cs = ckpt_scale ? ckpt_scale[0] : 1.0f;
-        const float inv = 1.0f / s;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = f32_to_e5m2((v[j] * cs) * inv);
+    for (int j = 0; j < kResRounds; ++j) {
+        const int blk = beg + j;
+        if (blk >= end) break;  // uniform over the workgroup
+        uint4* st = stage[j & 1];
+        st[lrow * kResLdsStride + lcol] = raw[j][0];
+        st[(lrow + 32) * kResLdsStride + lcol] = raw[j][1];
+        __syncthreads();
+        const int rb = blk / nkb;
+        const int g = (blk - rb * nkb) * 16 + sg;
+        const int n = rb * 64 + srow;
+        if (g < kg && n < N) {
+            const uint2 lo = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg], qs.inv, qs.cs);
+            const uint2 hi = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg + 1], qs.inv, qs.cs);
+            st_nt16(out + (static_cast<int64_t>(g) * N + n) * 16, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
     }
-    uint4 o;
-    o.x = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-    o.y = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
-    o.z = q[8] | (q[9] << 8) | (q[10] << 16) | (q[11] << 24);
-    o.w = q[12] | (q[13] << 8) | (q[14] << 16) | (q[15] << 24);
-    st_nt16(out + (static_cast<int64_t>(i) * N + n) * 16, o);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void* __restrict__ w, int N, int K,
+                                                                     const float* __restrict__ ckpt_scale, int native,
+                                                                     uint32_t* __restrict__ counters,
+                                                                     uint32_t* __restrict__ parts, int spin_limit,
+                                                                     uint8_t* __restrict__ out,
+                                                                     float* __restrict__ scale_out) {
+    static_assert(DT != kDtypeF32, "16-bit weights only");
+    __shared__ __attribute__((aligned(16))) uint4 stage[2][64 * kResLdsStride];
+    __shared__ uint32_t red[kResThreads / 64];
+    __shared__ int all_arrived;
+    const int tid = threadIdx.x;
+    const int G = static_cast<int>(gridDim.x);
+    const int kg = K >> 4;                 // 16-element K groups
+    const int nkb = (kg + 15) >> 4;        // 256-element K blocks
+    const int nblocks = nkb * ((N + 63) >> 6);
+    const int share = (nblocks + G - 1) / G;  // <= kResRounds (host check)
+    const int beg = static_cast<int>(blockIdx.x) * share;
+    const int end = beg + share < nblocks ? beg + share : nblocks;
+    const bool premul = !native;
+    const float cs = (premul && ckpt_scale) ? ckpt_scale[0] : 1.0f;
+    const bool per_element = premul && !(__builtin_fabsf(cs) <= 3.402823466e38f);  // inf or NaN scale
+
+    // load layout: thread tid holds 16-byte chunk tid & 31 of rows tid >> 5 and
+    // 32 + (tid >> 5) of each block (chunk = 8 elements; K % 16 == 0, so the
+    // two chunks of a K group are valid together)
+    const int lrow = tid >> 5;
+    const int lcol = tid & 31;
+    uint4 raw[kResRounds][2];
+#pragma unroll
+    for (int j = 0; j < kResRounds; ++j) {
+        raw[j][0] = raw[j][1] = make_uint4(0u, 0u, 0u, 0u);  // |0| leaves a maximum unchanged
+        const int blk = beg + j;
+        if (blk >= end) continue;
+        const int rb = blk / nkb;
+        const int k0 = (blk - rb * nkb) * 256 + lcol * 8;
+        if (k0 >= K) continue;
+        const int n0 = rb * 64 + lrow;
+        const uint16_t* base = static_cast<const uint16_t*>(w) + static_cast<int64_t>(n0) * K + k0;
+        if (n0 < N) raw[j][0] = ld_nt16(base);
+        if (n0 + 32 < N) raw[j][1] = ld_nt16(base + static_cast<int64_t>(32) * K);
+    }
+
+    // this workgroup's maximum, in the amax kernel's terms
+    uint32_t m = 0u;
+    if (!per_element) {
+#pragma unroll
+        for (int j = 0; j < kResRounds; ++j) m = abs_max_words<DT>(raw[j][1], abs_max_words<DT>(raw[j][0], m));
+        float a = abs_bits_to_f32<DT>(m);
+        if (premul) a = a * __builtin_fabsf(cs);
+        m = f32_bits(a) & 0x7fffffffu;
+    } else {
+        // x * cs per element; padding chunks are skipped (0 * inf would be NaN)
+#pragma unroll
+        for (int j = 0; j < kResRounds; ++j) {
+            const int blk = beg + j;
+            if (blk >= end) continue;
+            const int rb = blk / nkb;
+            if ((blk - rb * nkb) * 256 + lcol * 8 >= K) continue;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (rb * 64 + lrow + 32 * h >= N) continue;
+                const uint32_t wd[4] = {raw[j][h].x, raw[j][h].y, raw[j][h].z, raw[j][h].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t bits = static_cast<uint16_t>(e & 1 ? wd[e >> 1] >> 16 : wd[e >> 1] & 0xffffu);
+                    const float v = DT == kDtypeF16 ? half_bits_to_f32(bits) : bf16_bits_to_f32(bits);
+                    const uint32_t b = f32_bits(v * cs) & 0x7fffffffu;
+                    m = b > m ? b : m;
+                }
+            }
+        }
+    }
+    m = wave_max_u32(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const int xcd = static_cast<int>(blockIdx.x) % kResXcds;
+    const uint32_t xcd_size = static_cast<uint32_t>((G - xcd + kResXcds - 1) / kResXcds);
+    if (tid == 0) {
+        uint32_t r = red[0];
+        for (int k = 1; k < kResThreads / 64; ++k) r = red[k] > r ? red[k] : r;
+        __hip_atomic_store(&parts[blockIdx.x], r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial is visible before the arrival
+        if (__hip_atomic_fetch_add(&counters[res_arrive_word(xcd)], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == xcd_size - 1)
+            __hip_atomic_fetch_add(&counters[0], xcd_size, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int ok = 0;
+        for (int it = 0; it < spin_limit; ++it) {
+            if (__hip_atomic_load(&counters[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                static_cast<uint32_t>(G)) {
+                ok = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        all_arrived = ok;
+    }
+    __syncthreads();
+    m = 0u;
+    if (all_arrived) {
+        if (tid < G) m = __hip_atomic_load(&parts[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        // not every workgroup arrived in time: the whole weight's amax, alone
+        const int64_t nvec = static_cast<int64_t>(N) * K / 8;
+        const uint4* v16 = static_cast<const uint4*>(w);
+        if (!per_element) {
+            for (int64_t k = tid; k < nvec; k += kResThreads) m = abs_max_words<DT>(v16[k], m);
+            float a = abs_bits_to_f32<DT>(m);
+            if (premul) a = a * __builtin_fabsf(cs);
+            m = f32_bits(a) & 0x7fffffffu;
+        } else {
+            for (int64_t k = tid; k < nvec * 8; k += kResThreads) {
+                const uint32_t b = f32_bits(WeightType<DT>::load(w, k) * cs) & 0x7fffffffu;
+                m = b > m ? b : m;
+            }
+        }
+    }
+    m = wave_max_u32(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;  // thread 0 finished reading red[] before the barrier above
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int k = 1; k < kResThreads / 64; ++k) m = red[k] > m ? red[k] : m;
+    if (tid == 0 &&
+        __hip_atomic_fetch_add(&counters[res_depart_word(xcd)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            xcd_size - 1 &&
+        __hip_atomic_fetch_add(&counters[1], xcd_size, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            static_cast<uint32_t>(G) - xcd_size) {
+        // the last workgroup to leave: everyone has stopped polling and reading
+        __hip_atomic_store(&counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&counters[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int x = 0; x < kResXcds; ++x) {
+            __hip_atomic_store(&counters[res_arrive_word(x)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&counters[res_depart_word(x)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    const float s = scale_from_amax<DT>(m, native != 0);
+    if (scale_out && blockIdx.x == 0 && tid == 0) scale_out[0] = s;
+    const QuantScale qs = quant_scale<DT>(s, native != 0, cs, m < 0x7f800000u);
+    FEATHER_QUANT_MODES(qs.mode, (resident_store<DT, kM>(raw, stage, beg, end, nkb, kg, N, qs, out)))
 }
 
 // (N, K) bytes -> (K/16, N, 16) (dir 0) or back (dir 1): moves 16-byte chunks.
@@ -428,6 +709,30 @@ int grid_for(int64_t work, int per_block, int cap) {
     return static_cast<int>(g);
 }
 
+// FEATHEROPS_QUANT_RESIDENT=0 keeps the two-pass path everywhere;
+// FEATHEROPS_QUANT_SPIN sets the grid barrier's poll limit (tests force the
+// fallback with 0).
+bool resident_enabled() {
+    const char* e = std::getenv("FEATHEROPS_QUANT_RESIDENT");
+    return !(e && e[0] == '0');
+}
+
+int resident_spin_limit() {
+    const char* e = std::getenv("FEATHEROPS_QUANT_SPIN");
+    return e ? std::atoi(e) : 4096;
+}
+
+template <int DT>
+bool launch_quant_resident(const QuantArgs& q, hipStream_t stream) {
+    if (!q.counters || q.scale_in || q.cus <= 0 || q.cus > kResThreads || !resident_enabled()) return false;
+    const int64_t nblocks = ((q.K / 16 + 15) / 16) * ((q.N + 63) / 64);
+    if (nblocks > static_cast<int64_t>(q.cus) * kResRounds) return false;
+    hipLaunchKernelGGL((quant_resident_kernel<DT>), dim3(q.cus), dim3(kResThreads), 0, stream, q.w,
+                       static_cast<int>(q.N), static_cast<int>(q.K), q.ckpt_scale, q.native ? 1 : 0, q.counters,
+                       q.workspace, resident_spin_limit(), q.out, q.scale_out);
+    return true;
+}
+
 template <int DT>
 void launch_quant(const QuantArgs& q, hipStream_t stream) {
     const int64_t n = q.N * q.K;
@@ -451,8 +756,12 @@ void launch_quant(const QuantArgs& q, hipStream_t stream) {
 
 void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream) {
     switch (q.dtype) {
-        case kDtypeF16: launch_quant<kDtypeF16>(q, stream); break;
-        case kDtypeBF16: launch_quant<kDtypeBF16>(q, stream); break;
+        case kDtypeF16:
+            if (!launch_quant_resident<kDtypeF16>(q, stream)) launch_quant<kDtypeF16>(q, stream);
+            break;
+        case kDtypeBF16:
+            if (!launch_quant_resident<kDtypeBF16>(q, stream)) launch_quant<kDtypeBF16>(q, stream);
+            break;
         default: launch_quant<kDtypeF32>(q, stream); break;
     }
 }

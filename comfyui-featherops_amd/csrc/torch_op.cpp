@@ -361,15 +361,17 @@ std::tuple<at::Tensor, at::Tensor> quantize_prepack_e5m2(const at::Tensor& w, co
     const c10::DeviceGuard guard(src.device());
     at::Tensor out = at::empty({K / 16, N, 16}, src.options().dtype(at::kFloat8_e5m2));
     at::Tensor scale = at::empty({}, src.options().dtype(at::kFloat));
-    at::Tensor workspace = at::empty({256}, src.options().dtype(at::kInt));  // partial maxima (1 KB)
     at::Tensor cs;
     if (ckpt_scale.has_value()) cs = ckpt_scale->reshape({1}).to(src.device(), at::kFloat).contiguous();
     const hipStream_t stream = c10::hip::getCurrentHIPStream(src.device().index()).stream();
-    const int st = feather_quantize_prepack_e5m2(src.data_ptr(), code, N, K,
-                                                 cs.defined() ? static_cast<const float*>(cs.data_ptr()) : nullptr,
-                                                 native ? 1 : 0, static_cast<uint8_t*>(out.data_ptr()),
-                                                 static_cast<float*>(scale.data_ptr()),
-                                                 static_cast<uint32_t*>(workspace.data_ptr()), stream);
+    // the stream's zero-filled workspace (its counter region is left zero)
+    const size_t ws_bytes = feather_quantize_workspace_size();
+    at::Tensor& ws = workspace_for(src.device(), stream, ws_bytes);
+    const int st = feather_quantize_prepack_e5m2_ws(src.data_ptr(), code, N, K,
+                                                    cs.defined() ? static_cast<const float*>(cs.data_ptr()) : nullptr,
+                                                    native ? 1 : 0, static_cast<uint8_t*>(out.data_ptr()),
+                                                    static_cast<float*>(scale.data_ptr()), ws.data_ptr(),
+                                                    static_cast<size_t>(ws.numel()), stream);
     TORCH_CHECK(st == FEATHER_OK, "quantize_prepack failed: ", feather_status_string(st), " (status ", st, ")");
     return {out, scale};
 }

@@ -42,6 +42,9 @@ SIGNATURES: dict[str, tuple] = {
     "feather_scaled_mm_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "feather_scaled_mm_kernel_id": (_int, [_i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "feather_quantize_prepack_e5m2": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp]),
+    "feather_quantize_prepack_e5m2_ws": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp, _vp, _vp, ctypes.c_size_t,
+                                                 _vp]),
+    "feather_quantize_workspace_size": (ctypes.c_size_t, []),
     "feather_quantize_prepack_e5m2_scaled": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "feather_prepack_transpose": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "feather_unprepack_transpose": (_int, [_vp, _vp, _i64, _i64, _vp]),

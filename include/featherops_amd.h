@@ -214,6 +214,26 @@ int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t
                                   int native, uint8_t* out, float* scale_out, uint32_t* workspace, hipStream_t stream);
 
 /*
+ * Same as feather_quantize_prepack_e5m2, with the workspace contract of
+ * feather_launch_scaled_mm_ws: workspace_bytes >= feather_quantize_workspace_size(),
+ * the first 64 KB zero before the first call and left zero by every call (one
+ * zero-filled workspace serves this and the K-split GEMMs on one stream), the
+ * rest scratch. With it, fp16 / bf16 weights of up to 40 64x64 tiles per
+ * compute unit (80 MB of bf16 on an MI355X) take one pass: the weight is read
+ * once and kept in registers while the workgroups agree on the amax through
+ * two counters in the zero region (3 bytes of HBM traffic per element instead
+ * of 5); others take the two passes. Same results either way. Calls that
+ * share a workspace must not overlap (one stream). No counterpart in the
+ * reference: it replaces the same quant.py code as feather_quantize_prepack_e5m2.
+ */
+int feather_quantize_prepack_e5m2_ws(const void* w, int w_dtype, int64_t N, int64_t K, const float* ckpt_scale,
+                                     int native, uint8_t* out, float* scale_out, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes feather_quantize_prepack_e5m2_ws needs (64 KB + 4 KB). No counterpart in the reference. */
+size_t feather_quantize_workspace_size(void);
+
+/*
  * Same output with a caller-given scale (no amax, no clamp): q = e5m2(w *
  * T(1/scale)) in w's dtype T. Replaces quant.py:59-74 when `scale` is passed
  * to quantize_fp8e5m2_scaled. No workspace.
