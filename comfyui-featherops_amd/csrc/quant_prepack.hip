@@ -351,17 +351,20 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
     FEATHER_QUANT_MODES(qs.mode, st_nt16(dst, quant16<DT, kM>(v, qs.inv, qs.cs)))
 }
 
-// One-pass quantize for fp16 / bf16 weights that fit in the registers of one
-// workgroup per CU (kResRounds blocks of 64 rows x 256 elements per
-// workgroup: 80 MB of bf16 on 256 CUs). Each workgroup loads its blocks once
-// (each wave instruction two whole 512-byte row runs) and keeps them in VGPRs;
-// the workgroups exchange their partial maxima through a grid barrier (every
-// workgroup's partial is stored with a device-coherent store and acknowledged
-// before its arrival is counted; the partials are read only after all
-// arrivals are seen), then quantize from the registers, block by block through
-// LDS, so that each wave stores one K group of 64 consecutive rows (1 KB
-// contiguous in the (K/16, N, 16) layout): 3 bytes of HBM traffic per element
-// instead of the two-pass path's 5.
+// One-pass quantize for fp16 / bf16 weights: one workgroup per CU takes an
+// equal contiguous share of the weight's blocks (64 rows x 256 elements,
+// each wave load instruction two whole 512-byte row runs), keeps the first
+// kResRounds of them in VGPRs (80 MB of bf16 on 256 CUs) and reads the rest for
+// the amax only; the workgroups exchange their partial maxima through a grid
+// barrier (every workgroup's partial is stored with a device-coherent store
+// and acknowledged before its arrival is counted; the partials are read only
+// after all arrivals are seen), then quantize the register-held blocks, read
+// the rest again and quantize those, block by block through LDS so that each
+// wave stores one K group of 64 consecutive rows (1 KB contiguous in the
+// (K/16, N, 16) layout). HBM traffic per element: 3 bytes for weights that fit
+// the registers, 3 + 2 x (the share beyond them) otherwise, against the
+// two-pass path's 5. The element arithmetic is the two-pass path's, so the
+// codes are the same.
 //
 // The grid is one workgroup per CU, which a 1024-thread workgroup with this
 // register budget fills, so every workgroup is resident at once on an idle
@@ -386,32 +389,87 @@ constexpr int kResLdsStride = 33;  // 16-byte chunks per LDS row: 32 + 1 pad (co
 __host__ __device__ constexpr int res_arrive_word(int x) { return 64 * (1 + x); }
 __host__ __device__ constexpr int res_depart_word(int x) { return 64 * (1 + kResXcds + x); }
 
-// The store phase of quant_resident_kernel: round j's block goes through LDS
-// (stage[j & 1]; the barrier of round j + 1 orders round j's reads before
-// round j + 2's writes), wave g quantizes K group g of the block for rows
-// tid & 63 and stores them as 1 KB contiguous.
+// Chunk h (rows 0..31 or 32..63) of block blk for this thread: 16 bytes of
+// row blk / nkb * 64 + 32 h + tid / 32 at elements (blk % nkb) * 256 + 8 (tid % 32)
+// (K % 16 == 0, so the two chunks of a K group are valid together). Zero where
+// the block runs past the weight (|0| leaves a maximum unchanged).
+__device__ __forceinline__ bool chunk_valid(int blk, int h, int nkb, int N, int K) {
+    const int rb = blk / nkb;
+    return (blk - rb * nkb) * 256 + (threadIdx.x & 31) * 8 < K && rb * 64 + 32 * h + (threadIdx.x >> 5) < N;
+}
+__device__ __forceinline__ uint4 load_chunk(const void* w, int blk, int h, int nkb, int N, int K) {
+    const int tid = threadIdx.x;
+    const int rb = blk / nkb;
+    const int k0 = (blk - rb * nkb) * 256 + (tid & 31) * 8;
+    const int n = rb * 64 + 32 * h + (tid >> 5);
+    return k0 < K && n < N ? ld_nt16(static_cast<const uint16_t*>(w) + static_cast<int64_t>(n) * K + k0)
+                           : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// amax accumulation over one chunk: over the weight's own bits (scaled by
+// |ckpt_scale| once at the end), or per element over x * ckpt_scale for a
+// non-finite ckpt_scale (invalid chunks skipped: 0 * inf would be NaN)
+template <int DT>
+__device__ __forceinline__ uint32_t amax_chunk(uint4 r, bool valid, bool per_element, float cs, uint32_t m) {
+    if (!per_element) return abs_max_words<DT>(r, m);
+    if (!valid) return m;
+    const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint16_t bits = static_cast<uint16_t>(e & 1 ? wd[e >> 1] >> 16 : wd[e >> 1] & 0xffffu);
+        const float v = DT == kDtypeF16 ? half_bits_to_f32(bits) : bf16_bits_to_f32(bits);
+        const uint32_t b = f32_bits(v * cs) & 0x7fffffffu;
+        m = b > m ? b : m;
+    }
+    return m;
+}
+
+// One block of the store phase: through LDS (the caller alternates the two
+// stage buffers; the barrier of each block orders the reads of the block two
+// before), wave g quantizes K group g of the block for rows tid & 63 and
+// stores them as 1 KB contiguous.
+template <int DT, int kMode>
+__device__ __forceinline__ void store_block(uint4 c0, uint4 c1, uint4* st, int blk, int nkb, int kg, int N,
+                                            const QuantScale& qs, uint8_t* __restrict__ out) {
+    const int tid = threadIdx.x;
+    st[(tid >> 5) * kResLdsStride + (tid & 31)] = c0;
+    st[((tid >> 5) + 32) * kResLdsStride + (tid & 31)] = c1;
+    __syncthreads();
+    const int sg = tid >> 6, srow = tid & 63;
+    const int rb = blk / nkb;
+    const int g = (blk - rb * nkb) * 16 + sg;
+    const int n = rb * 64 + srow;
+    if (g < kg && n < N) {
+        const uint2 lo = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg], qs.inv, qs.cs);
+        const uint2 hi = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg + 1], qs.inv, qs.cs);
+        st_nt16(out + (static_cast<int64_t>(g) * N + n) * 16, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    }
+}
+
+// The store phase: the register-held blocks, then the blocks beyond them,
+// read again (kResStream at a time).
+constexpr int kResStream = 2;
 template <int DT, int kMode>
 __device__ __forceinline__ void resident_store(const uint4 (&raw)[kResRounds][2], uint4 (*stage)[64 * kResLdsStride],
-                                               int beg, int end, int nkb, int kg, int N, const QuantScale& qs,
-                                               uint8_t* __restrict__ out) {
-    const int tid = threadIdx.x;
-    const int lrow = tid >> 5, lcol = tid & 31;
-    const int sg = tid >> 6, srow = tid & 63;
+                                               const void* w, int beg, int end, int nkb, int kg, int N, int K,
+                                               const QuantScale& qs, uint8_t* __restrict__ out) {
 #pragma unroll
     for (int j = 0; j < kResRounds; ++j) {
-        const int blk = beg + j;
-        if (blk >= end) break;  // uniform over the workgroup
-        uint4* st = stage[j & 1];
-        st[lrow * kResLdsStride + lcol] = raw[j][0];
-        st[(lrow + 32) * kResLdsStride + lcol] = raw[j][1];
-        __syncthreads();
-        const int rb = blk / nkb;
-        const int g = (blk - rb * nkb) * 16 + sg;
-        const int n = rb * 64 + srow;
-        if (g < kg && n < N) {
-            const uint2 lo = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg], qs.inv, qs.cs);
-            const uint2 hi = quant8<DT, kMode>(st[srow * kResLdsStride + 2 * sg + 1], qs.inv, qs.cs);
-            st_nt16(out + (static_cast<int64_t>(g) * N + n) * 16, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        if (beg + j >= end) return;  // uniform over the workgroup
+        store_block<DT, kMode>(raw[j][0], raw[j][1], stage[j & 1], beg + j, nkb, kg, N, qs, out);
+    }
+    for (int blk0 = beg + kResRounds; blk0 < end; blk0 += kResStream) {
+        uint4 t[kResStream][2];
+#pragma unroll
+        for (int u = 0; u < kResStream; ++u) {
+            const int blk = blk0 + u < end ? blk0 + u : end - 1;
+            t[u][0] = load_chunk(w, blk, 0, nkb, N, K);
+            t[u][1] = load_chunk(w, blk, 1, nkb, N, K);
+        }
+#pragma unroll
+        for (int u = 0; u < kResStream; ++u) {
+            if (blk0 + u >= end) break;
+            store_block<DT, kMode>(t[u][0], t[u][1], stage[(blk0 - beg + u) & 1], blk0 + u, nkb, kg, N, qs, out);
         }
     }
 }
@@ -432,62 +490,45 @@ __global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void*
     const int kg = K >> 4;                 // 16-element K groups
     const int nkb = (kg + 15) >> 4;        // 256-element K blocks
     const int nblocks = nkb * ((N + 63) >> 6);
-    const int share = (nblocks + G - 1) / G;  // <= kResRounds (host check)
+    const int share = (nblocks + G - 1) / G;
     const int beg = static_cast<int>(blockIdx.x) * share;
     const int end = beg + share < nblocks ? beg + share : nblocks;
     const bool premul = !native;
     const float cs = (premul && ckpt_scale) ? ckpt_scale[0] : 1.0f;
     const bool per_element = premul && !(__builtin_fabsf(cs) <= 3.402823466e38f);  // inf or NaN scale
 
-    // load layout: thread tid holds 16-byte chunk tid & 31 of rows tid >> 5 and
-    // 32 + (tid >> 5) of each block (chunk = 8 elements; K % 16 == 0, so the
-    // two chunks of a K group are valid together)
-    const int lrow = tid >> 5;
-    const int lcol = tid & 31;
+    // the first kResRounds blocks stay in registers
     uint4 raw[kResRounds][2];
 #pragma unroll
-    for (int j = 0; j < kResRounds; ++j) {
-        raw[j][0] = raw[j][1] = make_uint4(0u, 0u, 0u, 0u);  // |0| leaves a maximum unchanged
-        const int blk = beg + j;
-        if (blk >= end) continue;
-        const int rb = blk / nkb;
-        const int k0 = (blk - rb * nkb) * 256 + lcol * 8;
-        if (k0 >= K) continue;
-        const int n0 = rb * 64 + lrow;
-        const uint16_t* base = static_cast<const uint16_t*>(w) + static_cast<int64_t>(n0) * K + k0;
-        if (n0 < N) raw[j][0] = ld_nt16(base);
-        if (n0 + 32 < N) raw[j][1] = ld_nt16(base + static_cast<int64_t>(32) * K);
-    }
-
+    for (int j = 0; j < kResRounds; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            raw[j][h] = beg + j < end ? load_chunk(w, beg + j, h, nkb, N, K) : make_uint4(0u, 0u, 0u, 0u);
     // this workgroup's maximum, in the amax kernel's terms
     uint32_t m = 0u;
     if (!per_element) {
 #pragma unroll
-        for (int j = 0; j < kResRounds; ++j) m = abs_max_words<DT>(raw[j][1], abs_max_words<DT>(raw[j][0], m));
+        for (int j = 0; j < kResRounds; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) m = abs_max_words<DT>(raw[j][h], m);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kResRounds; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                if (beg + j < end) m = amax_chunk<DT>(raw[j][h], chunk_valid(beg + j, h, nkb, N, K), true, cs, m);
+    }
+    // blocks beyond the registers: read for the amax now, again for the codes
+    for (int blk = beg + kResRounds; blk < end; ++blk) {
+        const uint4 t0 = load_chunk(w, blk, 0, nkb, N, K);
+        const uint4 t1 = load_chunk(w, blk, 1, nkb, N, K);
+        m = amax_chunk<DT>(t0, chunk_valid(blk, 0, nkb, N, K), per_element, cs, m);
+        m = amax_chunk<DT>(t1, chunk_valid(blk, 1, nkb, N, K), per_element, cs, m);
+    }
+    if (!per_element) {
         float a = abs_bits_to_f32<DT>(m);
         if (premul) a = a * __builtin_fabsf(cs);
         m = f32_bits(a) & 0x7fffffffu;
-    } else {
-        // x * cs per element; padding chunks are skipped (0 * inf would be NaN)
-#pragma unroll
-        for (int j = 0; j < kResRounds; ++j) {
-            const int blk = beg + j;
-            if (blk >= end) continue;
-            const int rb = blk / nkb;
-            if ((blk - rb * nkb) * 256 + lcol * 8 >= K) continue;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                if (rb * 64 + lrow + 32 * h >= N) continue;
-                const uint32_t wd[4] = {raw[j][h].x, raw[j][h].y, raw[j][h].z, raw[j][h].w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t bits = static_cast<uint16_t>(e & 1 ? wd[e >> 1] >> 16 : wd[e >> 1] & 0xffffu);
-                    const float v = DT == kDtypeF16 ? half_bits_to_f32(bits) : bf16_bits_to_f32(bits);
-                    const uint32_t b = f32_bits(v * cs) & 0x7fffffffu;
-                    m = b > m ? b : m;
-                }
-            }
-        }
     }
     m = wave_max_u32(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -556,7 +597,7 @@ __global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void*
     const float s = scale_from_amax<DT>(m, native != 0);
     if (scale_out && blockIdx.x == 0 && tid == 0) scale_out[0] = s;
     const QuantScale qs = quant_scale<DT>(s, native != 0, cs, m < 0x7f800000u);
-    FEATHER_QUANT_MODES(qs.mode, (resident_store<DT, kM>(raw, stage, beg, end, nkb, kg, N, qs, out)))
+    FEATHER_QUANT_MODES(qs.mode, (resident_store<DT, kM>(raw, stage, w, beg, end, nkb, kg, N, K, qs, out)))
 }
 
 // (N, K) bytes -> (K/16, N, 16) (dir 0) or back (dir 1): moves 16-byte chunks.
@@ -726,7 +767,7 @@ template <int DT>
 bool launch_quant_resident(const QuantArgs& q, hipStream_t stream) {
     if (!q.counters || q.scale_in || q.cus <= 0 || q.cus > kResThreads || !resident_enabled()) return false;
     const int64_t nblocks = ((q.K / 16 + 15) / 16) * ((q.N + 63) / 64);
-    if (nblocks > static_cast<int64_t>(q.cus) * kResRounds) return false;
+    if (nblocks >= (int64_t(1) << 30)) return false;  // block indices in int
     hipLaunchKernelGGL((quant_resident_kernel<DT>), dim3(q.cus), dim3(kResThreads), 0, stream, q.w,
                        static_cast<int>(q.N), static_cast<int>(q.K), q.ckpt_scale, q.native ? 1 : 0, q.counters,
                        q.workspace, resident_spin_limit(), q.out, q.scale_out);

@@ -1,6 +1,6 @@
 """The one-pass quantize (feather_quantize_prepack_e5m2_ws: each workgroup keeps
-its share of the weight in registers while the workgroups agree on the amax
-through a grid barrier) against the two-pass entry, feather_quantize_prepack_e5m2,
+its share of the weight in registers, the part beyond them read again, while
+the workgroups agree on the amax through a grid barrier) against the two-pass entry, feather_quantize_prepack_e5m2,
 and the oracle: codes and scale bit for bit, on the load path (fp32 arithmetic
 on w * ckpt_scale) and the patch path (the weight's dtype), with ragged
 shapes, special values, the barrier's timeout fallback forced from the host
@@ -56,8 +56,10 @@ def _same(a, b, what):
     assert torch.equal(qa, qb), f"{what}: codes differ"
 
 
+# up to (10240, 4096) every workgroup's share fits its registers (256 CUs);
+# (4100, 12304) (ragged in both) and (13824, 5120) read the rest of a share twice
 SHAPES = [(1, 16), (5, 48), (64, 64), (63, 80), (1000, 272), (3072, 3072), (5120, 5120), (2000, 9232),
-          (10240, 4096)]
+          (10240, 4096), (4100, 12304), (13824, 5120)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -124,7 +126,7 @@ def test_one_pass_special_values(cuda, dtype):
     assert (ws[:65536] == 0).all()
 
 
-@pytest.mark.parametrize("N,K", [(64, 64), (1000, 272), (3072, 3072)])
+@pytest.mark.parametrize("N,K", [(64, 64), (1000, 272), (3072, 3072), (4100, 12304)])
 def test_one_pass_barrier_fallback(cuda, monkeypatch, N, K):
     """FEATHEROPS_QUANT_SPIN=0: no workgroup waits for the others; each takes
     the amax over the whole weight itself. Same results, counters left zero."""

@@ -126,3 +126,26 @@ def test_protocol_checker_rejects_broken_orders(mutate):
     else:
         with pytest.raises(AssertionError):
             _check_protocol(mutate, body)
+
+
+def test_one_pass_quantize_barrier_order_in_compiled_code(tmp_path):
+    """quant_resident_kernel's grid barrier: each workgroup's partial maximum
+    is stored device-coherently (sc1) and acknowledged (vmcnt(0)) before its
+    returning arrival atomic; the partials are read (sc1 loads) only after the
+    wait loop has ended and a workgroup barrier has published its outcome."""
+    bodies = _bodies(_asm(tmp_path, "quant_prepack.hip"), r"quant_resident_kernel")
+    assert len(bodies) >= 2, f"found {len(bodies)} one-pass quantize kernels"
+    for name, body in bodies.items():
+        atomics = [i for i, s in enumerate(body) if re.match(r"global_atomic_add\S*\s", s)]
+        assert atomics, f"{name}: no arrival atomic"
+        a = atomics[0]
+        assert re.search(r"\bsc0\b", body[a]), f"{name}: the first arrival atomic does not return its result"
+        stores = [i for i in range(a) if re.match(r"global_store\S*\s", body[i]) and re.search(r"\bsc1\b", body[i])]
+        assert stores, f"{name}: no device-coherent partial store before the arrival"
+        assert any(_is_vmcnt0(s) for s in body[stores[-1] + 1:a]), f"{name}: the partial is not acknowledged first"
+        sleeps = [i for i in range(a, len(body)) if body[i].startswith("s_sleep")]
+        assert sleeps, f"{name}: no wait loop after the arrival"
+        bar = next((k for k in range(sleeps[-1], len(body)) if body[k] == "s_barrier"), None)
+        assert bar is not None, f"{name}: no barrier after the wait loop"
+        after = [k for k in range(bar, len(body)) if re.match(r"global_load\S*\s", body[k]) and re.search(r"\bsc1\b", body[k])]
+        assert after, f"{name}: no device-coherent partial loads after the barrier"
