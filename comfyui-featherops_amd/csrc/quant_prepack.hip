@@ -707,7 +707,8 @@ __global__ __launch_bounds__(256) void bf16_to_fp16_kernel(const uint16_t* __res
 }
 
 // dequantize (K/16, N, 16) e5m2 -> (N, K) in dtype T: T(float32(q) * s),
-// following quant.py:99-102 (FeatherFP8E5M2PackedLayout.dequantize).
+// following quant.py:99-102 (FeatherFP8E5M2PackedLayout.dequantize); fp32
+// outputs (fp16 / bf16 take dequant_rows_kernel below).
 template <int DT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ src, const float* __restrict__ scale,
                                                       void* __restrict__ dst, int N, int K) {
@@ -740,6 +741,70 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         uint4* d = reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst) + base);
         d[0] = make_uint4(o[0], o[1], o[2], o[3]);
         d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+}
+
+// The same for fp16 / bf16 outputs, block by block through LDS: a block is 64
+// rows x 256 elements (16 K groups); wave g reads K group g of the block's 64
+// rows (1 KB contiguous in the (K/16, N, 16) layout), converts it and puts
+// each row's 16 values into LDS; then each wave writes two whole 512-byte row
+// runs of the (N, K) output. Codes and output are streamed once (nontemporal
+// accesses). Element arithmetic as dequant_kernel. 13824 x 5120 -> fp16 on
+// MI355X: 41.6 us (5.1 TB/s on 3 B per element) against 78 us for
+// dequant_kernel's one-row-per-lane 32-byte writes (45.8 us with ordinary
+// loads and stores).
+constexpr int kDqLdsStride = 33;  // 16-byte chunks per LDS row: 32 + 1 pad
+template <int DT>
+__global__ __launch_bounds__(1024) void dequant_rows_kernel(const uint8_t* __restrict__ src,
+                                                            const float* __restrict__ scale,
+                                                            uint16_t* __restrict__ dst, int N, int K, int nkb) {
+    static_assert(DT != kDtypeF32, "16-bit outputs");
+    __shared__ __attribute__((aligned(16))) uint4 st[64 * kDqLdsStride];
+    const int tid = threadIdx.x;
+    const int blk = blockIdx.x;
+    const int rb = blk / nkb;
+    const int kb = blk - rb * nkb;
+    const int kg = K >> 4;
+    const float s = scale[0];
+    {
+        const int g = tid >> 6;     // K group within the block
+        const int row = tid & 63;   // row within the block
+        const int i = kb * 16 + g;
+        const int n = rb * 64 + row;
+        if (i < kg && n < N) {
+            const uint8_t* p = src + (static_cast<int64_t>(i) * N + n) * 16;
+            const uint4 raw = ld_nt16(p);
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint32_t o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                uint32_t half[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int q = 2 * j + e;
+                    const uint16_t h = static_cast<uint16_t>(((w[q >> 2] >> (8 * (q & 3))) & 0xffu) << 8);
+                    const float v = opaque_f32(half_bits_to_f32(h) * s);  // a -0 code stays -0
+                    half[e] = DT == kDtypeF16 ? f32_to_half_bits(v) : f32_to_bf16_bits(v);
+                }
+                o[j] = half[0] | (half[1] << 16);
+            }
+            st[row * kDqLdsStride + 2 * g] = make_uint4(o[0], o[1], o[2], o[3]);
+            st[row * kDqLdsStride + 2 * g + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+        }
+    }
+    __syncthreads();
+    const int c = tid & 31;        // 16-byte chunk of the row's 512-byte run
+    const int k = kb * 256 + c * 8;  // first element (K % 16 == 0: the chunk is whole when it starts inside)
+    if (k < K) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = (tid >> 5) + 32 * h;
+            const int n = rb * 64 + row;
+            if (n < N) {
+                uint16_t* q = dst + static_cast<int64_t>(n) * K + k;
+                st_nt16(q, st[row * kDqLdsStride + c]);
+            }
+        }
     }
 }
 
@@ -839,6 +904,20 @@ void launch_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, bool rne,
 
 void launch_dequant(const uint8_t* src, const float* scale, void* dst, int64_t N, int64_t K, int dtype,
                     hipStream_t stream) {
+    if (dtype != kDtypeF32) {
+        const int nkb = static_cast<int>((K / 16 + 15) / 16);
+        const int64_t nblocks = static_cast<int64_t>(nkb) * ((N + 63) / 64);
+        if (nblocks < (int64_t(1) << 31)) {
+            const dim3 g(static_cast<uint32_t>(nblocks));
+            uint16_t* d = static_cast<uint16_t*>(dst);
+            const int n32 = static_cast<int>(N), k32 = static_cast<int>(K);
+            if (dtype == kDtypeF16)
+                hipLaunchKernelGGL((dequant_rows_kernel<kDtypeF16>), g, dim3(1024), 0, stream, src, scale, d, n32, k32, nkb);
+            else
+                hipLaunchKernelGGL((dequant_rows_kernel<kDtypeBF16>), g, dim3(1024), 0, stream, src, scale, d, n32, k32, nkb);
+            return;
+        }
+    }
     const dim3 grid(static_cast<uint32_t>((K / 16 + 3) / 4), static_cast<uint32_t>((N + 63) / 64));
     switch (dtype) {
         case kDtypeF16:

@@ -147,12 +147,15 @@ def test_layout_kernels(cuda, quant, hk, N, K):
 
 @pytest.mark.parametrize("dtype,code", [(torch.float16, O.DT_F16), (torch.bfloat16, O.DT_BF16),
                                         (torch.float32, O.DT_F32)])
-def test_dequantize(cuda, quant, dtype, code):
-    rng = np.random.default_rng(3)
-    codes = rng.integers(0, 256, (96, 160), dtype=np.uint8)
+@pytest.mark.parametrize("N,K", [(96, 160), (1, 16), (63, 272), (130, 4112), (640, 2048)])
+def test_dequantize(cuda, quant, dtype, code, N, K):
+    """Every code value, ragged row blocks (N % 64) and K blocks (K % 256) of the block-wise kernel."""
+    rng = np.random.default_rng(3 + N + K)
+    codes = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    codes.reshape(-1)[:256] = np.arange(256, dtype=np.uint8)[: codes.size]
     packed = torch.from_numpy(O.prepack_transpose(codes)).view(torch.float8_e5m2).to(cuda)
     params = quant.FeatherFP8E5M2PackedParams(scale=torch.tensor(0.0123, device=cuda), orig_dtype=dtype,
-                                              orig_shape=(96, 160))
+                                              orig_shape=(N, K))
     out = quant.FeatherFP8E5M2PackedLayout.dequantize(packed, params)
     ref = O.dequantize(codes, np.float32(0.0123), code)
     got = out.cpu()
@@ -166,7 +169,7 @@ def test_dequantize(cuda, quant, dtype, code):
         assert np.array_equal(g[~np.isnan(g)], ref[~np.isnan(ref)])
         # signed zeros too: code 0x80 is -0 and must dequantize to -0
         assert np.array_equal(np.signbit(g[~np.isnan(g)]), np.signbit(ref[~np.isnan(ref)]))
-        assert np.signbit(g[codes == 0x80]).all() and (codes == 0x80).any()
+        assert np.signbit(g[codes == 0x80]).all() and (codes == 0x80).any() or codes.size < 129
     sd = quant.FeatherFP8E5M2PackedLayout.state_dict_tensors(packed, params)
     assert np.array_equal(_bytes(sd[""]), codes)
 
