@@ -686,7 +686,7 @@ def main() -> int:
         qbytes = Nq * Kq * (2 + 1)  # the weight read once, the e5m2 codes written once
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
         share = -(-((Kq // 16 + 15) // 16) * ((Nq + 63) // 64) // cus)  # 64 x 256 blocks per workgroup
-        hbm_per_elem = 3 + 2 * max(share - 10, 0) / share  # blocks beyond the 10 register-held ones read twice
+        hbm_per_elem = 3 + 2 * max(share - 12, 0) / share  # blocks beyond the 12 held (registers, LDS) read twice
         result["quantize"] = {"N": Nq, "K": Kq, "ms_per_weight": round(msq, 4),
                               "GB_per_s": round(qbytes / (msq * 1e-3) / 1e9, 1),
                               "pct_hbm_peak": round(100 * qbytes / (msq * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2),

@@ -354,16 +354,16 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
 // One-pass quantize for fp16 / bf16 weights: one workgroup per CU takes an
 // equal contiguous share of the weight's blocks (64 rows x 256 elements,
 // each wave load instruction two whole 512-byte row runs), keeps the first
-// kResRounds of them in VGPRs (80 MB of bf16 on 256 CUs) and reads the rest for
-// the amax only; the workgroups exchange their partial maxima through a grid
+// kResRounds of them in VGPRs (80 MB of bf16 on 256 CUs) and the next
+// kResLdsBlocks in LDS (16 MB more), and reads the rest for the amax only; the workgroups exchange their partial maxima through a grid
 // barrier (every workgroup's partial is stored with a device-coherent store
 // and acknowledged before its arrival is counted; the partials are read only
 // after all arrivals are seen), then quantize the register-held blocks, read
 // the rest again and quantize those, block by block through LDS so that each
 // wave stores one K group of 64 consecutive rows (1 KB contiguous in the
 // (K/16, N, 16) layout). HBM traffic per element: 3 bytes for weights that fit
-// the registers, 3 + 2 x (the share beyond them) otherwise, against the
-// two-pass path's 5. The element arithmetic is the two-pass path's, so the
+// the registers and LDS, 3 + 2 x (the share beyond them) otherwise, against
+// the two-pass path's 5. The element arithmetic is the two-pass path's, so the
 // codes are the same.
 //
 // The grid is one workgroup per CU, which a 1024-thread workgroup with this
@@ -382,6 +382,7 @@ __global__ __launch_bounds__(256) void quant_prepack_kernel(const void* __restri
 // workgroup, overwritten.
 constexpr int kResThreads = 1024;
 constexpr int kResRounds = 10;
+constexpr int kResLdsBlocks = 2;  // 64 KB of LDS beside the 67.6 KB of staging
 constexpr int kResXcds = 8;
 constexpr int kResLdsStride = 33;  // 16-byte chunks per LDS row: 32 + 1 pad (conflict-free column reads)
 // counter words: global arrivals, global departures, then per-XCD arrivals and
@@ -447,18 +448,26 @@ __device__ __forceinline__ void store_block(uint4 c0, uint4 c1, uint4* st, int b
 }
 
 // The store phase: the register-held blocks, then the blocks beyond them,
-// read again (kResStream at a time).
+// the blocks held in LDS, then the ones read again (kResStream at a time).
 constexpr int kResStream = 2;
 template <int DT, int kMode>
 __device__ __forceinline__ void resident_store(const uint4 (&raw)[kResRounds][2], uint4 (*stage)[64 * kResLdsStride],
-                                               const void* w, int beg, int end, int nkb, int kg, int N, int K,
-                                               const QuantScale& qs, uint8_t* __restrict__ out) {
+                                               const uint4 (*held)[2 * kResThreads], const void* w, int beg, int end,
+                                               int nkb, int kg, int N, int K, const QuantScale& qs,
+                                               uint8_t* __restrict__ out) {
 #pragma unroll
     for (int j = 0; j < kResRounds; ++j) {
         if (beg + j >= end) return;  // uniform over the workgroup
         store_block<DT, kMode>(raw[j][0], raw[j][1], stage[j & 1], beg + j, nkb, kg, N, qs, out);
     }
-    for (int blk0 = beg + kResRounds; blk0 < end; blk0 += kResStream) {
+#pragma unroll
+    for (int e = 0; e < kResLdsBlocks; ++e) {
+        const int j = kResRounds + e;
+        if (beg + j >= end) return;
+        store_block<DT, kMode>(held[e][threadIdx.x], held[e][kResThreads + threadIdx.x], stage[j & 1], beg + j, nkb,
+                               kg, N, qs, out);
+    }
+    for (int blk0 = beg + kResRounds + kResLdsBlocks; blk0 < end; blk0 += kResStream) {
         uint4 t[kResStream][2];
 #pragma unroll
         for (int u = 0; u < kResStream; ++u) {
@@ -483,6 +492,7 @@ __global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void*
                                                                      float* __restrict__ scale_out) {
     static_assert(DT != kDtypeF32, "16-bit weights only");
     __shared__ __attribute__((aligned(16))) uint4 stage[2][64 * kResLdsStride];
+    __shared__ __attribute__((aligned(16))) uint4 held[kResLdsBlocks][2 * kResThreads];
     __shared__ uint32_t red[kResThreads / 64];
     __shared__ int all_arrived;
     const int tid = threadIdx.x;
@@ -518,8 +528,21 @@ __global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void*
             for (int h = 0; h < 2; ++h)
                 if (beg + j < end) m = amax_chunk<DT>(raw[j][h], chunk_valid(beg + j, h, nkb, N, K), true, cs, m);
     }
-    // blocks beyond the registers: read for the amax now, again for the codes
-    for (int blk = beg + kResRounds; blk < end; ++blk) {
+    // the next kResLdsBlocks blocks wait in LDS (each thread keeps its own two
+    // chunks: no barrier needed to read them back)
+#pragma unroll
+    for (int e = 0; e < kResLdsBlocks; ++e) {
+        const int blk = beg + kResRounds + e;
+        if (blk >= end) break;
+        const uint4 t0 = load_chunk(w, blk, 0, nkb, N, K);
+        const uint4 t1 = load_chunk(w, blk, 1, nkb, N, K);
+        m = amax_chunk<DT>(t0, chunk_valid(blk, 0, nkb, N, K), per_element, cs, m);
+        m = amax_chunk<DT>(t1, chunk_valid(blk, 1, nkb, N, K), per_element, cs, m);
+        held[e][tid] = t0;
+        held[e][kResThreads + tid] = t1;
+    }
+    // blocks beyond those: read for the amax now, again for the codes
+    for (int blk = beg + kResRounds + kResLdsBlocks; blk < end; ++blk) {
         const uint4 t0 = load_chunk(w, blk, 0, nkb, N, K);
         const uint4 t1 = load_chunk(w, blk, 1, nkb, N, K);
         m = amax_chunk<DT>(t0, chunk_valid(blk, 0, nkb, N, K), per_element, cs, m);
@@ -597,7 +620,7 @@ __global__ __launch_bounds__(kResThreads) void quant_resident_kernel(const void*
     const float s = scale_from_amax<DT>(m, native != 0);
     if (scale_out && blockIdx.x == 0 && tid == 0) scale_out[0] = s;
     const QuantScale qs = quant_scale<DT>(s, native != 0, cs, m < 0x7f800000u);
-    FEATHER_QUANT_MODES(qs.mode, (resident_store<DT, kM>(raw, stage, w, beg, end, nkb, kg, N, K, qs, out)))
+    FEATHER_QUANT_MODES(qs.mode, (resident_store<DT, kM>(raw, stage, held, w, beg, end, nkb, kg, N, K, qs, out)))
 }
 
 // (N, K) bytes -> (K/16, N, 16) (dir 0) or back (dir 1): moves 16-byte chunks.

@@ -219,8 +219,8 @@ int feather_quantize_prepack_e5m2(const void* w, int w_dtype, int64_t N, int64_t
  * the first 64 KB zero before the first call and left zero by every call (one
  * zero-filled workspace serves this and the K-split GEMMs on one stream), the
  * rest scratch. With it, fp16 / bf16 weights take one pass: one workgroup per
- * compute unit keeps its share of the weight in registers (up to 80 MB of bf16
- * on an MI355X; the rest of a larger share is read twice) while the
+ * compute unit keeps its share of the weight in registers and LDS (up to 96 MB
+ * of bf16 on an MI355X; the rest of a larger share is read twice) while the
  * workgroups agree on the amax through counters in the zero region (3 bytes of
  * HBM traffic per element instead of 5 for weights that fit); fp32 weights
  * take the two passes. Same results either way. Calls that

@@ -56,10 +56,11 @@ def _same(a, b, what):
     assert torch.equal(qa, qb), f"{what}: codes differ"
 
 
-# up to (10240, 4096) every workgroup's share fits its registers (256 CUs);
-# (4100, 12304) (ragged in both) and (13824, 5120) read the rest of a share twice
+# on 256 CUs: up to (10240, 4096) every workgroup's share fits its registers,
+# (11264, 4096) needs the LDS as well, (4100, 12304) (ragged in both) and
+# (13824, 5120) read the rest of a share twice
 SHAPES = [(1, 16), (5, 48), (64, 64), (63, 80), (1000, 272), (3072, 3072), (5120, 5120), (2000, 9232),
-          (10240, 4096), (4100, 12304), (13824, 5120)]
+          (10240, 4096), (11264, 4096), (4100, 12304), (13824, 5120)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
