@@ -54,7 +54,7 @@ constexpr int kBK = 64;
 
 // kLora: 0 = none, 1 = fp16 factors, 2 = bf16 factors (T is M x R, U is N x R,
 // both row-major with R % 32 == 0 and 16-byte aligned rows)
-template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, bool kABf16, int kLora>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, int kLora>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
         for (int rm = 0; rm < RM; ++rm) {
             hook(rm);
-            const half8_t a = a_frag<kABf16>(araw[rm]);
+            const half8_t a = a_frag<false>(araw[rm]);
 #pragma unroll
             for (int j = 0; j < RN; ++j) {
                 // serpentine over the N repeats: consecutive MFMAs change only
@@ -564,12 +564,12 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
     const int c_nt = p.M * p.N * 2 > (int64_t(256) << 20) ? 1 : 0;
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
-#define FEATHER_LDS_LAUNCH_L(BF, E4, AB, LORA)                                                                        \
-    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, AB, LORA>), grid, block, 0,      \
+#define FEATHER_LDS_LAUNCH_L(BF, E4, LORA)                                                                            \
+    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, LORA>), grid, block, 0,          \
                        stream, p.a, p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),          \
                        static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, partials,   \
                        counters, p.lora_t, p.lora_u, static_cast<int>(p.lora_rank), c_nt)
-#define FEATHER_LDS_LAUNCH(BF, E4, AB) FEATHER_LDS_LAUNCH_L(BF, E4, AB, 0)
+#define FEATHER_LDS_LAUNCH(BF, E4) FEATHER_LDS_LAUNCH_L(BF, E4, 0)
     if (p.lora_dtype != 0) {
         // rank-R epilogue: the default schedule's large tiles, fp16 activations,
         // e5m2 weights, no K split
@@ -577,36 +577,30 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
         if constexpr (PIPE == 1 && BM >= 128 && BM * 128 + BN * 64 >= (BM > BN ? BM : BN) * 128) {
             if (p.a_bf16 || p.b_e4m3 || ksplit != 1) return false;
             if (p.lora_dtype == 1) {
-                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, false, 1);
-                else FEATHER_LDS_LAUNCH_L(false, false, false, 1);
+                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, 1);
+                else FEATHER_LDS_LAUNCH_L(false, false, 1);
             } else {
-                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, false, 2);
-                else FEATHER_LDS_LAUNCH_L(false, false, false, 2);
+                if (p.out_bf16) FEATHER_LDS_LAUNCH_L(true, false, 2);
+                else FEATHER_LDS_LAUNCH_L(false, false, 2);
             }
             return true;
         }
         return false;
     }
-    if (p.a_bf16) {
-        // bf16 activations: the small split-K tiles only (default schedule, e5m2
-        // weights). On the large tiles, where every A fragment is read by 2-4
-        // waves, converting each read costs more than a separate cast pass
-        // (measured at M=32768 N=13824 K=5120: 4.44 ms vs 3.68 ms cast + GEMM),
-        // so the caller converts A for them.
-        if constexpr (PIPE == 1 && BM <= 64) {
-            if (p.b_e4m3) return false;
-            if (p.out_bf16) FEATHER_LDS_LAUNCH(true, false, true);
-            else FEATHER_LDS_LAUNCH(false, false, true);
-            return true;
-        }
-        return false;
-    }
+    // bf16 activations: none of these tiles; the caller rounds A to fp16 first.
+    // Converting each A fragment as it is read costs more than a separate cast
+    // pass on every tile here, because each fragment is read by 2-4 waves and
+    // feeds only 1-6 MFMAs (graph-replayed, bf16 out, M=512 N=3072 K=12288 on
+    // the 64 x 64 split-K tiles: 102 us converted in the kernel vs 60 us cast
+    // first, fp16 A 54 us; M=4096 N=3072 K=3072 on the 128 x 384 tile: 68 vs
+    // 66 us; M=32768 N=13824 K=5120 on the 256 x 256 tile: 4.44 vs 3.68 ms).
+    if (p.a_bf16) return false;
     if (p.out_bf16) {
-        if (p.b_e4m3) FEATHER_LDS_LAUNCH(true, true, false);
-        else FEATHER_LDS_LAUNCH(true, false, false);
+        if (p.b_e4m3) FEATHER_LDS_LAUNCH(true, true);
+        else FEATHER_LDS_LAUNCH(true, false);
     } else {
-        if (p.b_e4m3) FEATHER_LDS_LAUNCH(false, true, false);
-        else FEATHER_LDS_LAUNCH(false, false, false);
+        if (p.b_e4m3) FEATHER_LDS_LAUNCH(false, true);
+        else FEATHER_LDS_LAUNCH(false, false);
     }
 #undef FEATHER_LDS_LAUNCH
 #undef FEATHER_LDS_LAUNCH_L

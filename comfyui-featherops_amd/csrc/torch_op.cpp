@@ -172,9 +172,9 @@ void scaled_mm(const at::Tensor& a, const at::Tensor& b_prepacked, const std::op
 
 // feather_ops::scaled_mm_any_m: any row count M without padding (the kernels
 // mask rows past M), the tile from feather_scaled_mm_pick_config, fp16 or bf16
-// activations. bf16 activations are rounded to fp16 inside the kernel where it
-// has that variant, otherwise by the library's round-to-nearest-even cast
-// first: the values of x.to(float16) (comfy_feather/ops.py:88) either way.
+// activations. bf16 activations are rounded to fp16 inside the small-M kernel,
+// otherwise by the library's round-to-nearest-even cast first: the values of
+// x.to(float16) (comfy_feather/ops.py:88) either way.
 at::Tensor scaled_mm_any_m(const at::Tensor& a, const at::Tensor& b_prepacked, const std::optional<at::Tensor>& scale,
                            const std::optional<at::Tensor>& bias, at::ScalarType out_dtype) {
     TORCH_CHECK(a.dim() == 2, "a must be 2D");
