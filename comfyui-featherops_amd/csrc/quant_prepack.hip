@@ -636,6 +636,42 @@ __global__ __launch_bounds__(256) void chunk_transpose_kernel(const uint8_t* __r
     else *reinterpret_cast<uint4*>(dst + row_major) = *reinterpret_cast<const uint4*>(src + packed);
 }
 
+// The same, block by block through LDS: a block is 64 rows x 16 K groups
+// (256 bytes of each row); the row-major side moves whole 256-byte row runs
+// (four per wave instruction), the packed side one K group of 64 consecutive
+// rows (1 KB) per wave instruction. dir 0: (N, K) -> (K/16, N, 16); dir 1 back.
+constexpr int kCtLdsStride = 17;  // 16-byte chunks per LDS row: 16 + 1 pad
+template <int kDir>
+__global__ __launch_bounds__(1024) void chunk_transpose_rows_kernel(const uint8_t* __restrict__ src,
+                                                                    uint8_t* __restrict__ dst, int N, int K, int nkb) {
+    __shared__ uint4 st[64 * kCtLdsStride];
+    const int tid = threadIdx.x;
+    const int rb = static_cast<int>(blockIdx.x) / nkb;
+    const int kb = static_cast<int>(blockIdx.x) - rb * nkb;
+    const int kg = K >> 4;
+    // row-major side: row tid / 16 of the block, chunk (K group) tid % 16
+    const int rrow = tid >> 4, rc = tid & 15;
+    const int rn = rb * 64 + rrow;
+    const int rk = kb * 256 + rc * 16;
+    const bool rvalid = rn < N && rk < K;
+    // packed side: K group tid / 64 of the block, row tid % 64
+    const int pg = tid >> 6, prow = tid & 63;
+    const int pi = kb * 16 + pg;
+    const int pn = rb * 64 + prow;
+    const bool pvalid = pi < kg && pn < N;
+    const int64_t row_major = static_cast<int64_t>(rn) * K + rk;
+    const int64_t packed = (static_cast<int64_t>(pi) * N + pn) * 16;
+    if (kDir == 0) {
+        if (rvalid) st[rrow * kCtLdsStride + rc] = ld_nt16(src + row_major);
+        __syncthreads();
+        if (pvalid) st_nt16(dst + packed, st[prow * kCtLdsStride + pg]);
+    } else {
+        if (pvalid) st[prow * kCtLdsStride + pg] = ld_nt16(src + packed);
+        __syncthreads();
+        if (rvalid) st_nt16(dst + row_major, st[rrow * kCtLdsStride + rc]);
+    }
+}
+
 // (K, N) bytes -> (K/16, N, 16): P[i, n, j] = B[16 i + j, n]. One thread per
 // (i, 4 columns): 16 row loads of 4 bytes, a byte transpose in registers, one
 // 64-byte contiguous write.
@@ -896,6 +932,18 @@ void launch_quantize_prepack(const QuantArgs& q, hipStream_t stream) {
 }
 
 void launch_chunk_transpose(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int dir, hipStream_t stream) {
+    const int nkb = static_cast<int>((K / 16 + 15) / 16);
+    const int64_t nblocks = static_cast<int64_t>(nkb) * ((N + 63) / 64);
+    if (nblocks < (int64_t(1) << 31)) {
+        const dim3 g(static_cast<uint32_t>(nblocks));
+        if (dir == 0)
+            hipLaunchKernelGGL(chunk_transpose_rows_kernel<0>, g, dim3(1024), 0, stream, src, dst, static_cast<int>(N),
+                               static_cast<int>(K), nkb);
+        else
+            hipLaunchKernelGGL(chunk_transpose_rows_kernel<1>, g, dim3(1024), 0, stream, src, dst, static_cast<int>(N),
+                               static_cast<int>(K), nkb);
+        return;
+    }
     const dim3 grid(static_cast<uint32_t>((K / 16 + 3) / 4), static_cast<uint32_t>((N + 63) / 64));
     hipLaunchKernelGGL(chunk_transpose_kernel, grid, dim3(256), 0, stream, src, dst, static_cast<int>(N),
                        static_cast<int>(K), dir);

@@ -132,7 +132,7 @@ def test_special_inputs(cuda, quant):
         quant.FeatherFP8E5M2PackedLayout.quantize(torch.randn(16, device=cuda))
 
 
-@pytest.mark.parametrize("N,K", [(1, 16), (5, 48), (64, 64), (1000, 272), (3072, 3072)])
+@pytest.mark.parametrize("N,K", [(1, 16), (5, 48), (64, 64), (63, 4112), (1000, 272), (3072, 3072)])
 def test_layout_kernels(cuda, quant, hk, N, K):
     rng = np.random.default_rng(N + K)
     w = rng.integers(0, 256, (N, K), dtype=np.uint8)
