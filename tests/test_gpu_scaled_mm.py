@@ -309,7 +309,8 @@ def test_workspace_shared_across_shapes(cuda):
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 1024), (16, 12288, 512), (48, 1024, 2048), (64, 1024, 1024),
                                    (256, 768, 512), (1024, 4096, 1024), (100, 512, 1040), (4096, 4096, 4096),
-                                   (4096, 3072, 3072), (1000, 5120, 640), (4608, 3072, 3072)])
+                                   (4096, 3072, 3072), (1000, 5120, 640), (4608, 3072, 3072), (2048, 2048, 64),
+                                   (1024, 1536, 128), (3000, 2304, 320)])
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
 def test_bf16_activations(cuda, hk, M, N, K, out_dtype):
     """bf16 A through the any-M entry: rounded to fp16 inside the kernel (or cast
@@ -616,3 +617,4 @@ def test_small_m_lean_stage_counts(cuda, M, N, K):
     torch.cuda.synchronize()
     ref = O.scaled_mm_ref(a.numpy(), packed, s, bias_np, O.DT_F16)
     assert_gemm_close(c, ref, torch.float16, f"lean {M}x{N}x{K}")
+
