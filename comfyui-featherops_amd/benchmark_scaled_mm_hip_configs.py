@@ -22,17 +22,10 @@ from pathlib import Path
 
 import torch
 
-if __package__ in (None, ""):
-    # the plugin folder's name is not an identifier: import it as `featherops_amd`
-    import importlib.util
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+from _bench_common import load_plugin, time_calls  # noqa: E402
 
-    _root = Path(__file__).resolve().parent
-    _spec = importlib.util.spec_from_file_location("featherops_amd", _root / "__init__.py",
-                                                   submodule_search_locations=[str(_root)])
-    _pkg = importlib.util.module_from_spec(_spec)
-    sys.modules["featherops_amd"] = _pkg
-    _spec.loader.exec_module(_pkg)
-
+load_plugin()
 from featherops_amd.kernel.hip.hip_kernel import (  # noqa: E402
     _CONFIGS, any_m_config, kernel_id, prepack_b_for_scaled_mm, scaled_mm_hip_any_m, scaled_mm_hip_configured)
 from featherops_amd.kernel.hip.utils import _config_compatible  # noqa: E402
@@ -49,29 +42,6 @@ def _parse_tuples(text: str, width: int, what: str) -> list[tuple[int, ...]]:
             raise ValueError(f"Invalid {what} '{chunk}', expected {width} comma-separated ints")
         out.append(tuple(int(p) for p in parts))
     return out
-
-
-def _time_all(fn, warmup_ms: float, rep_ms: float) -> list[float]:
-    """Per-call milliseconds of fn, HIP events around each call after ~warmup_ms of calls."""
-    fn()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(5):
-        fn()
-    e.record()
-    e.synchronize()
-    est = max(s.elapsed_time(e) / 5, 1e-3)
-    for _ in range(max(1, int(warmup_ms / est))):
-        fn()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(max(1, int(rep_ms / est)))]
-    for a, b in evs:
-        a.record()
-        fn()
-        b.record()
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs]
 
 
 def main() -> None:
@@ -108,7 +78,7 @@ def main() -> None:
             runs.append((f"any_m pick=({','.join(map(str, pick))})", kernel_id(m, n, k, pick),
                          lambda: scaled_mm_hip_any_m(a, bp, scale, bias, out_dtype)))
         for label, kid, fn in runs:
-            t = _time_all(fn, args.warmup, args.rep)
+            t = time_calls(fn, args.warmup, args.rep)
             avg = statistics.mean(t)
             std = statistics.pstdev(t) if len(t) > 1 else 0.0
             print(f"  {label} kernel={kid} avg_ms={avg:.3f} std_ms={std:.3f} "

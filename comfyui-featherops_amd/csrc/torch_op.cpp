@@ -394,6 +394,30 @@ at::Tensor quantize_prepack_e5m2_scaled(const at::Tensor& w, const at::Tensor& s
     return out;
 }
 
+// feather_ops::bf16_to_fp16: the bf16 -> fp16 casts of kernel/convert.py,
+// registered in C++ so that a call costs one dispatch (small tensors are bound
+// by the host). rne = false: the reference's round-toward-zero cast
+// (kernel/convert.py:24-34, saturating at +-65504; the Python entry keeps its
+// even-length assertion, the kernel takes any length); rne = true: round to
+// nearest even, the values of x.to(torch.float16).
+at::Tensor bf16_to_fp16(const at::Tensor& x, bool rne) {
+    TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16");
+    TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(x.data_ptr()) % 16 == 0, "x data pointer must be 16-byte aligned");
+    at::Tensor out = at::empty(x.sizes(), x.options().dtype(at::kHalf));
+    if (x.numel() == 0) return out;
+    const c10::DeviceGuard guard(x.device());
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    const auto* in = static_cast<const uint16_t*>(x.data_ptr());
+    auto* o = static_cast<uint16_t*>(out.data_ptr());
+    const int st = rne ? feather_bf16_to_fp16_rne(in, o, x.numel(), stream) : feather_bf16_to_fp16(in, o, x.numel(), stream);
+    TORCH_CHECK(st == FEATHER_OK, "bf16_to_fp16 failed: ", feather_status_string(st), " (status ", st, ")");
+    return out;
+}
+
+at::Tensor bf16_to_fp16_meta(const at::Tensor& x, bool) { return at::empty(x.sizes(), x.options().dtype(at::kHalf)); }
+
 at::Tensor scaled_mm_any_m_meta(const at::Tensor& a, const at::Tensor& b_prepacked,
                                 const std::optional<at::Tensor>& scale, const std::optional<at::Tensor>& bias,
                                 at::ScalarType out_dtype) {
@@ -411,6 +435,7 @@ TORCH_LIBRARY(feather_ops, m) {
     m.def("quantize_prepack_e5m2(Tensor w, Tensor? ckpt_scale, bool native) -> (Tensor, Tensor)");
     m.def("quantize_prepack_e5m2_scaled(Tensor w, Tensor scale) -> Tensor");
     m.def("lora_down(Tensor x, Tensor d) -> Tensor");
+    m.def("bf16_to_fp16(Tensor x, bool rne) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
@@ -420,12 +445,14 @@ TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("quantize_prepack_e5m2", &quantize_prepack_e5m2);
     m.impl("quantize_prepack_e5m2_scaled", &quantize_prepack_e5m2_scaled);
     m.impl("lora_down", &lora_down);
+    m.impl("bf16_to_fp16", &bf16_to_fp16);
 }
 
 TORCH_LIBRARY_IMPL(feather_ops, Meta, m) {
     m.impl("scaled_mm_any_m", &scaled_mm_any_m_meta);
     m.impl("scaled_mm_any_m_lora", &scaled_mm_any_m_lora_meta);
     m.impl("lora_down", &lora_down_meta);
+    m.impl("bf16_to_fp16", &bf16_to_fp16_meta);
 }
 
 // the reference's Python custom op of this name, as a C++ op (the namespace

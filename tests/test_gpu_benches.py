@@ -1,6 +1,8 @@
-"""The benchmark harnesses that mirror the reference's (cpp_benchmarks/ and
-benchmark_scaled_mm_hip_configs.py) run and report: the libtorch C++ bench with its
-float64 check of the output, and the per-config sweep over every compatible tuple."""
+"""The benchmark harnesses that mirror the reference's (cpp_benchmarks/ and the
+plugin-root scripts benchmark_scaled_mm_hip_configs.py, benchmark_scaled_mm_hip.py,
+benchmark_convert.py, profile_scaled_mm_hip.py) run and report: the libtorch C++
+bench with its float64 check of the output, the per-config sweep over every
+compatible tuple, the square-size and cast sweeps, and the profiling workload."""
 
 import re
 import subprocess
@@ -67,3 +69,27 @@ def test_hbm_copy_floor_both_launch_methods():
     plain = _run([exe, "--read-bytes", 4 << 20])
     graph = _run([exe, "--read-bytes", 4 << 20, "--graph"])
     assert re.search(r"us/call", plain) and "(graph replay)" in graph
+
+
+def test_square_sweep_script():
+    text = _run([sys.executable, "benchmark_scaled_mm_hip.py", "--sizes", "128,512", "--rep", "3", "--warmup", "1"],
+                cwd=PKG)
+    rows = [ln.split() for ln in text.splitlines() if re.match(r"^\s+\d+\s+[0-9.]+\s+[0-9.]+\s*$", ln)]
+    assert [int(r[0]) for r in rows] == [128, 512], text
+    assert all(float(v) > 0 for r in rows for v in r[1:]), text
+
+
+def test_convert_sweep_script():
+    text = _run([sys.executable, "benchmark_convert.py", "--sizes", "1024,2048", "--rep", "3", "--warmup", "1"],
+                cwd=PKG)
+    rows = [ln.split() for ln in text.splitlines() if re.match(r"^\s+\d+(\s+[0-9.]+){3}\s*$", ln)]
+    assert [int(r[0]) for r in rows] == [1024, 2048], text
+    assert all(float(v) > 0 for r in rows for v in r[1:]), text
+
+
+def test_profile_script():
+    text = _run([sys.executable, "profile_scaled_mm_hip.py", "-N", "512", "--iters", "2"], cwd=PKG)
+    assert "runs kernel" in text and text.rstrip().endswith("Done"), text
+    text = _run([sys.executable, "profile_scaled_mm_hip.py", "-N", "256", "--iters", "1", "--config", "2,4,4,8,4",
+                 "--no-scale", "--no-bias"], cwd=PKG)
+    assert text.rstrip().endswith("Done"), text

@@ -3,6 +3,8 @@ the bf16 -> fp16 cast against the oracle and the golden fixtures."""
 
 import hashlib
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -215,6 +217,13 @@ def test_bf16_to_fp16_rne_exhaustive(cuda, pkg):
     out = torch.empty(xr.shape, dtype=torch.float16, device=cuda)
     assert lib().feather_bf16_to_fp16_rne(xr.data_ptr(), out.data_ptr(), xr.numel(), stream(cuda)) == 0
     assert torch.equal(out, xr.to(torch.float16))
+    # the Python entry (kernel.convert.bf16_to_fp16_rne), odd length and 2-D shape kept
+    conv = importlib.import_module(f"{pkg.__name__}.kernel.convert")
+    for shape in ((65536,), (3, 7), (1000, 999)):
+        x = (torch.randn(shape, dtype=torch.float32) * 3e4).bfloat16().to(cuda)
+        y = conv.bf16_to_fp16_rne(x)
+        assert y.shape == x.shape and y.dtype == torch.float16
+        assert torch.equal(y.view(torch.int16), x.to(torch.float16).view(torch.int16)), shape
 
 
 def test_bf16_to_fp16_large_streaming_path(cuda):

@@ -180,9 +180,31 @@ def test_native_op_registered_in_cpp(hk):
                               "-> (Tensor, Tensor)")
     qs = torch.ops.feather_ops.quantize_prepack_e5m2_scaled.default
     assert str(qs._schema) == "feather_ops::quantize_prepack_e5m2_scaled(Tensor w, Tensor scale) -> Tensor"
-    for op_ in (q, qs):
+    cv = torch.ops.feather_ops.bf16_to_fp16.default
+    assert str(cv._schema) == "feather_ops::bf16_to_fp16(Tensor x, bool rne) -> Tensor"
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(cv.name(), "Meta")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key(cv.name(), "CPU")
+    for op_ in (q, qs, cv):
         assert torch._C._dispatch_has_kernel_for_dispatch_key(op_.name(), "CUDA")
         assert "csrc/torch_op.cpp" in torch._C._dispatch_dump(op_.name())
+
+
+def test_convert_entries_keep_reference_checks(pkg):
+    """kernel/convert.py keeps the reference's assertions (bf16, contiguous, even
+    length for the RTZ cast) and refuses host tensors before any launch."""
+    import importlib
+
+    conv = importlib.import_module(f"{pkg.__name__}.kernel.convert")
+    with pytest.raises(AssertionError):
+        conv.bf16_to_fp16(torch.zeros(4, dtype=torch.float16))
+    with pytest.raises(AssertionError):
+        conv.bf16_to_fp16(torch.zeros(4, 4, dtype=torch.bfloat16).t())
+    with pytest.raises(AssertionError):
+        conv.bf16_to_fp16(torch.zeros(3, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        conv.bf16_to_fp16_rne(torch.zeros(3, dtype=torch.bfloat16))
+    meta = torch.ops.feather_ops.bf16_to_fp16.default(torch.empty(5, 6, dtype=torch.bfloat16, device="meta"), True)
+    assert meta.shape == (5, 6) and meta.dtype == torch.float16
 
 
 def test_op_library_loads_first_in_fresh_process():
