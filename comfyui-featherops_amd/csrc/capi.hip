@@ -49,7 +49,7 @@ int tile_kernel_for(int64_t M, int64_t K, int wm, int wn, int rm, int rn) {
     if (bm == 128 && bn == 384) return lds ? feather::kLds128x384 : feather::kTile128x128;
     if (bm >= 256 && bn >= 256) {
         if (!lds) return feather::kTile256x256;
-        return wm > wn ? feather::kLds256x256w4x2 : feather::kLds256x256w2x4;
+        return feather::kLds256x256;
     }
     if (bm >= 256) return lds ? feather::kLds256x128 : feather::kTile256x128;
     if (bn >= 256) return bm >= 128 ? (lds ? feather::kLds128x256 : feather::kTile128x256) : feather::kTile64x128;
@@ -227,7 +227,7 @@ bool feather_launch_scaled_mm_ex(const void* a, int a_dtype, const uint8_t* b_pr
     p.smallm_min_groups = tuning_smallm_groups();
     if (is_splitk(kid)) return feather::launch_lds_splitk(p, workspace, workspace_bytes, stream);
     if (kid == feather::kSmallM) return feather::launch_smallm_kernel(p, workspace, workspace_bytes, stream);
-    if (kid >= feather::kLds256x256w2x4) return feather::launch_lds_kernel(kid, p, stream);
+    if (kid >= feather::kLds256x256) return feather::launch_lds_kernel(kid, p, stream);
     return feather::launch_tile_kernel(kid, p, stream);
 }
 
@@ -238,7 +238,7 @@ bool feather_launch_scaled_mm_lora(const void* a, const uint8_t* b_prepacked, co
                                    int b_dtype, int output_dtype, hipStream_t stream) {
     const int kid = feather_scaled_mm_kernel_id(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n);
     // the rank-R epilogue exists on the large LDS tiles (fp16 activations, e5m2 weights)
-    if (kid < feather::kLds256x256w2x4 || is_splitk(kid)) return false;
+    if (kid < feather::kLds256x256 || is_splitk(kid)) return false;
     if (b_dtype != FEATHER_B_E5M2 || (output_dtype != 0 && output_dtype != 1)) return false;
     if (lora_dtype != FEATHER_DTYPE_F16 && lora_dtype != FEATHER_DTYPE_BF16) return false;
     if (lora_t == nullptr || lora_u == nullptr || rank <= 0 || rank % 32 != 0 || rank > INT32_MAX / 2) return false;

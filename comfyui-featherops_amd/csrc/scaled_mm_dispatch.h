@@ -39,8 +39,7 @@ enum KernelId : int {
     kTile64x64 = 6,
     kSmallM = 10,  // M <= 64: K split inside the workgroup (and across workgroups with a workspace), 16- or 64-column strips
     // LDS-DMA pipelined tiles (K % 64 == 0)
-    kLds256x256w2x4 = 20,
-    kLds256x256w4x2 = 21,
+    kLds256x256 = 20,  // both 256 x 256 tuples (2,4,4,8,4) and (4,2,4,4,8)
     kLds256x128 = 22,
     kLds128x256 = 23,
     kLds128x128 = 24,

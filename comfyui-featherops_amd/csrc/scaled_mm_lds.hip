@@ -211,7 +211,60 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // Changing the activation operand costs more than changing the weight
     // operand (an e5m2 byte widens to an fp16 with a zero low byte): running the M
     // repeats innermost measured 4% slower.
-    auto mm_half = [&](int kh, const uint4 (&araw)[RM], const uint4 (&braw)[RN], auto hook) {
+    // Pinned schedule (the 256 x 256 tile, e5m2 weights, default schedule):
+    // each weight column is widened just before it is first needed, in
+    // program order with the MFMAs (both inline asm, so neither moves), instead
+    // of a whole K half's columns in one burst ahead of its first MFMA; the
+    // MFMAs run in a serpentine over the columns, and the next K half's first
+    // two columns are widened during this half's last repeat once they are
+    // free. M=32768 N=13824 K=5120 on MI355X: 3.268 vs 3.315 ms (median of
+    // alternating runs; 8192^3 0.765 vs 0.774 ms), the same bits. Ordering
+    // rules the asm keeps by construction (the compiler's hazard tracking does
+    // not see inside asm): a widened column is written at least two MFMAs
+    // before an MFMA reads it and overwritten at least three MFMAs after its
+    // last read, and the accumulators are read by other instructions only
+    // after the wait states that follow the main loop.
+    constexpr bool kPinned = kPipe == 1 && !kE4m3 && BM == 256 && BN == 256 && RM % 2 == 0 && RN >= 4;
+    auto widen_pinned = [](uint32_t lo, uint32_t hi) -> half8_t {
+        uint32_t w0, w1, w2, w3;
+        asm volatile(
+            "v_perm_b32 %0, 0, %4, %6\n\t"
+            "v_perm_b32 %1, 0, %4, %7\n\t"
+            "v_perm_b32 %2, 0, %5, %6\n\t"
+            "v_perm_b32 %3, 0, %5, %7"
+            : "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
+            : "v"(lo), "v"(hi), "s"(0x010c000cu), "s"(0x030c020cu));
+        return __builtin_bit_cast(half8_t, make_uint4(w0, w1, w2, w3));
+    };
+    half8_t bqp[RN];  // pinned schedule: the current K half's widened columns
+    auto mm_half = [&](int kh, const uint4 (&araw)[RM], const uint4 (&braw)[RN], auto hook, bool pre = false) {
+        if constexpr (kPinned) {
+            // MFMA j of repeat rm uses column col(kh, rm, j): forward or
+            // reversed by repeat, K half 1 starting reversed, so the columns the
+            // next half needs first are the ones this half's last repeat uses
+            // first. pre: widen the next half's first two columns here (braw
+            // holds the next stage's weights by then when kh == 1).
+            auto col = [](int h, int rm, int j) { return (((rm & 1) ^ h) != 0) ? RN - 1 - j : j; };
+            auto wd = [&](int rn, int h) {
+                bqp[rn] = h == 0 ? widen_pinned(braw[rn].x, braw[rn].y) : widen_pinned(braw[rn].z, braw[rn].w);
+            };
+            constexpr int kPre = RN >= 6 ? RN / 2 : 2;
+#pragma unroll
+            for (int rm = 0; rm < RM; ++rm) {
+                hook(rm);
+                const half8_t a = a_frag<false>(araw[rm]);
+#pragma unroll
+                for (int j = 0; j < RN; ++j) {
+                    if (rm == 0 && j + 2 < RN) wd(col(kh, 0, j + 2), kh);
+                    if (rm == RM - 1 && pre && (j == kPre || j == kPre + 1)) wd(col(kh ^ 1, 0, j - kPre), kh ^ 1);
+                    const int rn = col(kh, rm, j);
+                    f32x4 t = acc[rm][rn];
+                    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(t) : "v"(bqp[rn]), "v"(a));
+                    acc[rm][rn] = t;
+                }
+            }
+            return;
+        }
         half8_t bq[RN];
 #pragma unroll
         for (int rn = 0; rn < RN; ++rn)
@@ -254,6 +307,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         stage_barrier();
         read_b(S0{}, braw);
         read_a(S0{}, 0, araw[0]);
+        if constexpr (kPinned) {
+            // K half 0 of stage 0 starts forward: columns 0 and 1
+            static_assert(RM / 4 >= 1, "the next stage's weights arrive after repeat 0");
+            bqp[0] = widen_pinned(braw[0].x, braw[0].y);
+            bqp[1] = widen_pinned(braw[1].x, braw[1].y);
+        }
         // kFull: stages kt + 1 and kt + 2 exist (no bounds checks, so the
         // steady-state loop body has no branches around the copies)
         auto run_stage = [&](auto cur, auto full, int kt) {
@@ -268,7 +327,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
 #pragma unroll
                 for (int i = 0; i < kLoadsPerStage; ++i)
                     if (rm == (i * RM) / kLoadsPerStage && has2) issue_one(Free{}, kt + 2, i);
-            });
+            }, true);
             // mm_half widens braw before the first hook, so the hook may
             // overwrite braw with the next stage's operands
             mm_half(1, araw[1], braw, [&](int rm) {
@@ -280,7 +339,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
                     read_b(Next{}, braw);
                     read_a(Next{}, 0, araw[0]);
                 }
-            });
+            }, has1);
         };
         using Full = std::true_type;
         using Tail = std::false_type;
@@ -324,6 +383,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         }
     }
 
+    // pinned schedule: wait states between the last asm MFMA and any other
+    // instruction that reads its accumulator
+    if constexpr (kPinned) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     const float s = has_scale ? scale[0] : 1.0f;
     // (K split: only the 32- and 64-row tiles are ever launched with ksplit > 1)
     if constexpr (BM <= 64) if (ksplit > 1) {
@@ -611,8 +673,11 @@ template <int PIPE>
 bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks = 1, float* partials = nullptr,
                      uint32_t* counters = nullptr) {
     switch (kernel_id) {
-        case kLds256x256w2x4: return launch_lds<256, 256, 2, 4, PIPE>(p, stream);
-        case kLds256x256w4x2: return launch_lds<256, 256, 4, 2, PIPE>(p, stream);
+        // 256 x 256: 4 x 2 waves (64 x 128 wave tiles) with the pinned schedule for
+        // e5m2 weights; e4m3fn weights (widened by a conversion instruction,
+        // compiler-scheduled) keep 2 x 4 waves, the faster layout there
+        case kLds256x256:
+            return p.b_e4m3 ? launch_lds<256, 256, 2, 4, PIPE>(p, stream) : launch_lds<256, 256, 4, 2, PIPE>(p, stream);
         case kLds256x128: return launch_lds<256, 128, 4, 2, PIPE>(p, stream);
         case kLds128x256: return launch_lds<128, 256, 2, 4, PIPE>(p, stream);
         case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
