@@ -618,3 +618,41 @@ def test_small_m_lean_stage_counts(cuda, M, N, K):
     ref = O.scaled_mm_ref(a.numpy(), packed, s, bias_np, O.DT_F16)
     assert_gemm_close(c, ref, torch.float16, f"lean {M}x{N}x{K}")
 
+
+
+LARGE_TILE_CFGS = [(2, 4, 4, 8, 4), (4, 2, 4, 4, 8), (4, 2, 4, 4, 4), (2, 4, 4, 8, 3), (2, 4, 4, 4, 6), (2, 4, 4, 4, 4),
+                   (2, 2, 4, 4, 4)]
+
+
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 320, 1088])
+@pytest.mark.parametrize("b_dtype", [torch.float8_e5m2, torch.float8_e4m3fn])
+def test_large_tiles_every_stage_count(cuda, monkeypatch, K, b_dtype):
+    """Every large LDS tile from one 64-K stage up: the first stage, the steady three-stage
+    loop and its 1-, 2- and 3-stage tails take different code, and on e5m2 weights the
+    widening and MFMAs there are ordered by hand (each K half's first two weight columns
+    widened during the previous half's last repeat, none after the last stage). All configs
+    must give the same bits (the K order of every sum is the same), M and N not multiples of
+    the tiles, and match a float64 evaluation of the whole output."""
+    monkeypatch.setenv("FEATHEROPS_SPLITK", "0")  # this grid would otherwise take the split-K tiles
+    M, N = 777, 1152
+    g = torch.Generator().manual_seed(K)
+    a = torch.randn(M, K, generator=g).half().to(cuda)
+    fmax = 448.0 if b_dtype == torch.float8_e4m3fn else 57344.0
+    w = torch.randn(N, K, generator=g) * 0.02
+    s = (w.abs().max() / fmax).float().reshape(1)
+    bp = (w / s).to(b_dtype).view(N, K // 16, 16).permute(1, 0, 2).contiguous().to(cuda)
+    sd = s.to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.1).half().to(cuda)
+    ref = torch_ref_dev(a, bp, sd, bias, torch.float16, b_dtype=b_dtype)
+    first = None
+    for cfg in LARGE_TILE_CFGS:
+        kid = lib().feather_scaled_mm_kernel_id(M, N, K, *cfg)
+        print("large tile", M, N, K, cfg, "kernel", kid, b_dtype, flush=True)
+        assert 20 <= kid <= 26, f"{cfg} maps to kernel {kid}, not a large LDS tile"
+        y = capi_scaled_mm(a, bp.view(torch.uint8), sd, bias, torch.float16, cfg,
+                           b_dtype=0 if b_dtype == torch.float8_e4m3fn else 1)
+        assert_gemm_close_dev(y, ref, torch.float16, f"{cfg} K={K}")
+        if first is None:
+            first = y
+        else:
+            assert torch.equal(y.view(torch.int16), first.view(torch.int16)), f"{cfg} K={K} differs from {LARGE_TILE_CFGS[0]}"
