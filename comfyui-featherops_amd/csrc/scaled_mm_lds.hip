@@ -211,8 +211,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // Changing the activation operand costs more than changing the weight
     // operand (an e5m2 byte widens to an fp16 with a zero low byte): running the M
     // repeats innermost measured 4% slower.
-    // Pinned schedule (e5m2 weights, default schedule, wave tiles of at least
-    // 64 x 64):
+    // Pinned schedule (default schedule, wave tiles of at least 64 x 64):
     // each weight column is widened just before it is first needed, in
     // program order with the MFMAs (both inline asm, so neither moves), instead
     // of a whole K half's columns in one burst ahead of its first MFMA; the
@@ -223,22 +222,35 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // vs 0.774 ms; M=4096 N=3072 K=3072 (128 x 384) 56.2 vs 57.8 us, K=12288
     // 209.8 vs 213.7 us (256 x 192 on 4 x 2 waves: 210.3 vs 217.1 us on 2 x 4);
     // M=2048 N=K=4096: 128 x 256 52.0 vs 52.8 us, 256 x 128 53.3 vs 54.9 us,
-    // 128 x 128 62.9 vs 63.6 us. Ordering
+    // 128 x 128 62.9 vs 63.6 us; e4m3fn weights at M=32768 N=13824 K=5120
+    // 3.225 vs 3.251 ms (4 x 2 pinned vs 2 x 4 compiler-scheduled). Ordering
     // rules the asm keeps by construction (the compiler's hazard tracking does
     // not see inside asm): a widened column is written at least two MFMAs
     // before an MFMA reads it and overwritten at least three MFMAs after its
     // last read, and the accumulators are read by other instructions only
     // after the wait states that follow the main loop.
-    constexpr bool kPinned = kPipe == 1 && !kE4m3 && RM % 2 == 0 && RM >= 4 && RN >= 4;
+    constexpr bool kPinned = kPipe == 1 && RM % 2 == 0 && RM >= 4 && RN >= 4;
+    // widen_fp8x8's instructions as asm (e5m2: byte shuffles; e4m3fn: the
+    // hardware fp8 -> fp16 conversion with scale 1, low then high word)
     auto widen_pinned = [](uint32_t lo, uint32_t hi) -> half8_t {
         uint32_t w0, w1, w2, w3;
-        asm volatile(
-            "v_perm_b32 %0, 0, %4, %6\n\t"
-            "v_perm_b32 %1, 0, %4, %7\n\t"
-            "v_perm_b32 %2, 0, %5, %6\n\t"
-            "v_perm_b32 %3, 0, %5, %7"
-            : "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
-            : "v"(lo), "v"(hi), "s"(0x010c000cu), "s"(0x030c020cu));
+        if constexpr (!kE4m3) {
+            asm volatile(
+                "v_perm_b32 %0, 0, %4, %6\n\t"
+                "v_perm_b32 %1, 0, %4, %7\n\t"
+                "v_perm_b32 %2, 0, %5, %6\n\t"
+                "v_perm_b32 %3, 0, %5, %7"
+                : "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
+                : "v"(lo), "v"(hi), "s"(0x010c000cu), "s"(0x030c020cu));
+        } else {
+            asm volatile(
+                "v_cvt_scalef32_pk_f16_fp8 %0, %4, 1.0\n\t"
+                "v_cvt_scalef32_pk_f16_fp8 %1, %4, 1.0 op_sel:[1,0,0]\n\t"
+                "v_cvt_scalef32_pk_f16_fp8 %2, %5, 1.0\n\t"
+                "v_cvt_scalef32_pk_f16_fp8 %3, %5, 1.0 op_sel:[1,0,0]"
+                : "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
+                : "v"(lo), "v"(hi));
+        }
         return __builtin_bit_cast(half8_t, make_uint4(w0, w1, w2, w3));
     };
     half8_t bqp[RN];  // pinned schedule: the current K half's widened columns
@@ -678,17 +690,14 @@ template <int PIPE>
 bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks = 1, float* partials = nullptr,
                      uint32_t* counters = nullptr) {
     switch (kernel_id) {
-        // 256 x 256 and 256 x 192: 4 x 2 waves (64 x 128 / 64 x 96 wave tiles,
-        // the pinned schedule) for e5m2 weights; e4m3fn weights (widened by a
-        // conversion instruction, compiler-scheduled) keep 2 x 4 waves, the
-        // faster layout there
-        case kLds256x256:
-            return p.b_e4m3 ? launch_lds<256, 256, 2, 4, PIPE>(p, stream) : launch_lds<256, 256, 4, 2, PIPE>(p, stream);
+        // 256 x 256 and 256 x 192 on 4 x 2 waves (64 x 128 / 64 x 96 wave tiles:
+        // 20% fewer LDS operand bytes per stage than 2 x 4, and wide enough
+        // for the pinned schedule)
+        case kLds256x256: return launch_lds<256, 256, 4, 2, PIPE>(p, stream);
         case kLds256x128: return launch_lds<256, 128, 4, 2, PIPE>(p, stream);
         case kLds128x256: return launch_lds<128, 256, 2, 4, PIPE>(p, stream);
         case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
-        case kLds256x192:
-            return p.b_e4m3 ? launch_lds<256, 192, 2, 4, PIPE>(p, stream) : launch_lds<256, 192, 4, 2, PIPE>(p, stream);
+        case kLds256x192: return launch_lds<256, 192, 4, 2, PIPE>(p, stream);
         case kLds128x384: return launch_lds<128, 384, 2, 4, PIPE>(p, stream);
         case kLdsSk64x64: return launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters);
         case kLdsSk32x128: return launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
