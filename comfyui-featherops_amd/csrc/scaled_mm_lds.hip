@@ -226,9 +226,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // 3.225 vs 3.251 ms (4 x 2 pinned vs 2 x 4 compiler-scheduled). Ordering
     // rules the asm keeps by construction (the compiler's hazard tracking does
     // not see inside asm): a widened column is written at least two MFMAs
-    // before an MFMA reads it and overwritten at least three MFMAs after its
-    // last read, and the accumulators are read by other instructions only
-    // after the wait states that follow the main loop.
+    // before an MFMA reads it (the register of one an MFMA has read may be
+    // rewritten right after it, as the compiler's own code for builtin MFMAs
+    // does), the MFMAs accumulate in place with nothing else touching the
+    // accumulators in the loop, and other instructions read the accumulators
+    // only after the wait states that follow the main loop (all checked on the
+    // compiled code by tests/test_pinned_codegen.py).
     constexpr bool kPinned = kPipe == 1 && RM % 2 == 0 && RM >= 4 && RN >= 4;
     // widen_fp8x8's instructions as asm (e5m2: byte shuffles; e4m3fn: the
     // hardware fp8 -> fp16 conversion with scale 1, low then high word)
