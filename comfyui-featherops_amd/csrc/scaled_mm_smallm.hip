@@ -277,10 +277,21 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     const int n0 = blockIdx.x * 16;
     const int nst = K >> 6;
 
-    const float s = has_scale ? scale[0] : 1.0f;
-    // lane c < 16 of every wave holds the bias of column n0 + c (read by the
-    // epilogue lanes through a shuffle)
-    const uint16_t bias_c = has_bias && lane < 16 ? bias[n0 + lane] : static_cast<uint16_t>(0);
+    // The scale and lane c's bias value (column n0 + c % 16; the epilogue
+    // lanes read it through a shuffle) are loaded first, as vector loads with
+    // no branch around them (an absent scale or bias reads A's first bytes and
+    // is not used), so nothing waits for them before the stream starts: they
+    // complete ahead of the round's copies and weights, in issue order, and
+    // are selected in the epilogue. (Read under has_scale / has_bias, the
+    // compiler waited for both -- a memory round trip -- before issuing the
+    // first copy; a scalar load of the scale would be waited for with the
+    // kernel arguments.)
+    const uint32_t scale_raw = __builtin_amdgcn_raw_buffer_load_b32(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(has_scale ? static_cast<const void*>(scale)
+                                                                      : static_cast<const void*>(A)),
+                                          0, 4, 0x00020000),
+        0, 0, 0);
+    const uint16_t bias_raw = *(has_bias ? bias + n0 + (lane & 15) : A);
 
     // copy j of a stage: rows 8 j .. 8 j + 7, lane -> (row 8 j + lane / 8, chunk lane % 8);
     // the swizzle depends on row % 16 only
@@ -360,6 +371,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
         }
     }
 
+    const float s = has_scale ? __uint_as_float(scale_raw) : 1.0f;
+    const uint16_t bias_c = has_bias ? bias_raw : static_cast<uint16_t>(0);
     __syncthreads();  // the reduction buffer overlays other waves' slabs
     float* red = reinterpret_cast<float*>(smem);  // [wave][row][kRedStride]
 #pragma unroll
