@@ -104,6 +104,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
+    // The scale, loaded before anything else by a vector load with no branch
+    // around it (an absent scale reads A's first bytes and is not used) and
+    // selected in the epilogue: it is in long before the epilogue needs it
+    // (read there, the scalar load's round trip came before the staging), and
+    // as the oldest load it never holds up the stage waits below, which leave
+    // only younger copies in flight.
+    const uint32_t scale_raw = __builtin_amdgcn_raw_buffer_load_b32(
+        __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void*>(has_scale ? static_cast<const void*>(scale) : static_cast<const void*>(A)), 0, 4,
+            0x00020000),
+        0, 0, 0);
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -406,7 +417,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     // pinned schedule: wait states between the last asm MFMA and any other
     // instruction that reads its accumulator
     if constexpr (kPinned) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-    const float s = has_scale ? scale[0] : 1.0f;
+    // the scale into a scalar register here, where the main loop has already
+    // waited for every load (the memory clobber keeps the epilogue's bias load
+    // from being issued before this wait, so the bias still lands behind the
+    // staging writes)
+    uint32_t scale_s;
+    asm volatile("v_readfirstlane_b32 %0, %1" : "=s"(scale_s) : "v"(scale_raw) : "memory");
+    const float s = has_scale ? __uint_as_float(scale_s) : 1.0f;
     // (K split: only the 32- and 64-row tiles are ever launched with ksplit > 1)
     if constexpr (BM <= 64) if (ksplit > 1) {
         // ---- K split: each workgroup writes its fp32 accumulators to the
