@@ -269,6 +269,11 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     constexpr int kRedStride = 17;
     static_assert(kWaves * 16 * MT * kRedStride * 4 <= kWaves * U * kStageSlab, "reduction fits the slabs");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kWaves * U * kStageSlab];
+    // one row tile: the cross-wave reduction buffer beside the slabs (17 KB;
+    // 145 KB in all), so a wave writes its sums as soon as it is done; two
+    // row tiles overlay it on the slabs (there is no room beside them)
+    constexpr bool kOwnRed = MT == 1;
+    __shared__ __attribute__((aligned(16))) float red_own[kOwnRed ? kWaves * 16 * MT * kRedStride : 1];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -277,8 +282,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     const int n0 = blockIdx.x * 16;
     const int nst = K >> 6;
 
-    // The scale and lane c's bias value (column n0 + c % 16; the epilogue
-    // lanes read it through a shuffle) are loaded first, as vector loads with
+    // The scale and lane l's bias value (column n0 + l % 16, the column the
+    // epilogue thread on that lane stores) are loaded first, as vector loads with
     // no branch around them (an absent scale or bias reads A's first bytes and
     // is not used), so nothing waits for them before the stream starts: they
     // complete ahead of the round's copies and weights, in issue order, and
@@ -373,8 +378,8 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
 
     const float s = has_scale ? __uint_as_float(scale_raw) : 1.0f;
     const uint16_t bias_c = has_bias ? bias_raw : static_cast<uint16_t>(0);
-    __syncthreads();  // the reduction buffer overlays other waves' slabs
-    float* red = reinterpret_cast<float*>(smem);  // [wave][row][kRedStride]
+    if constexpr (!kOwnRed) __syncthreads();  // the reduction buffer overlays other waves' slabs
+    float* red = kOwnRed ? red_own : reinterpret_cast<float*>(smem);  // [wave][row][kRedStride]
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -382,11 +387,11 @@ __global__ __launch_bounds__(64 * kWaves) void scaled_mm_m16_kernel(const uint16
     __syncthreads();
     if (tid < 256 * MT) {
         const int r = tid >> 4;
-        const int c = tid & 15;
+        const int c = tid & 15;  // = lane & 15: this lane's bias_c is column n0 + c's
         float sum = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) sum += red[(w * 16 * MT + r) * kRedStride + c];
-        const uint16_t b = static_cast<uint16_t>(__shfl(static_cast<int>(bias_c), c));
+        const uint16_t b = bias_c;
         if (r < M) {
             uint16_t o = f32_to_out_bits<kBf16>(opaque_f32(sum * s));
             if (has_bias) o = f32_to_out_bits<kBf16>(out_bits_to_f32<kBf16>(o) + out_bits_to_f32<kBf16>(b));
