@@ -78,6 +78,7 @@ struct SplitKPlan {
     int tiles;
     size_t counter_bytes;   // the fixed counter region (kWorkspaceCounterBytes) when ksplit > 1
     size_t workspace_bytes; // counter region + ksplit fp32 partial tiles per output tile
+    int stages;             // LDS stage ring depth of the default schedule (5 or 6)
 };
 SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target);
 // Same workspace contract as launch_smallm_kernel.

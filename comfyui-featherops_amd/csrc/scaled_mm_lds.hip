@@ -49,12 +49,21 @@
 namespace feather {
 namespace {
 
+// f(std::integral_constant<int, i>{}) for i = 0 .. N-1, in order
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 constexpr int kBK = 64;
 
 
 // kLora: 0 = none, 1 = fp16 factors, 2 = bf16 factors (T is M x R, U is N x R,
 // both row-major with R % 32 == 0 and 16-byte aligned rows)
-template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, int kLora>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int kPipe, bool kBf16, bool kE4m3, int kLora, int kStages>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int has_scale, int has_bias,
@@ -79,10 +88,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     constexpr int kBPerWave = (kBInst + kWaves - 1) / kWaves;
     constexpr int kLoadsPerStage = kAPerWave + kBPerWave;
     static_assert(BN % 64 == 0, "a B copy must stay inside one K group");
-    // One LDS object per stage buffer (the main loop is unrolled by three).
+    // One LDS object per stage buffer for the first three (the main loop is
+    // unrolled by the stage count); deeper rings add buffers behind them.
+    static_assert(kStages == 3 || (kPipe == 1 && kStages >= 4 && kStages <= 8), "stage ring depth");
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t sbuf2[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t sbufx[kStages > 3 ? (kStages - 3) * kStage : 1024];
 
     // ---- tile index: XCD-contiguous grouped raster; the K splits of a tile
     // are consecutive in that order (so mostly on one XCD) ----
@@ -156,7 +168,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         constexpr int b = decltype(tag)::value;
         if constexpr (b == 0) return sbuf0;
         else if constexpr (b == 1) return sbuf1;
-        else return sbuf2;
+        else if constexpr (b == 2) return sbuf2;
+        else return sbufx + (b - 3) * kStage;
     };
     // LDS byte address of stage buffer `tag` (a constant)
     auto stage_lds = [&](auto tag) -> uint32_t { return lds_addr_of(stage_buf(tag)); };
@@ -328,12 +341,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         constexpr int kBarrierRm = RM / 4;
         uint4 araw[2][RM];
         uint4 braw[RN];
+        // Deeper rings (kStages > 3) always keep kStages - 1 stages of copies
+        // issued: a stage past the end copies stage nk - 1 again into its
+        // (never read) buffer, so every wait count is a constant and no
+        // branch surrounds a copy; the main loop waits for those copies
+        // before the epilogue reuses the buffers.
         issue_stage(S0{}, 0);
-        if (nk > 1) {
-            issue_stage(S1{}, 1);
-            wait_vmcnt<kLoadsPerStage>();
+        if constexpr (kStages == 3) {
+            if (nk > 1) {
+                issue_stage(S1{}, 1);
+                wait_vmcnt<kLoadsPerStage>();
+            } else {
+                wait_vmcnt<0>();
+            }
         } else {
-            wait_vmcnt<0>();
+            static_for<kStages - 2>([&](auto i) {
+                constexpr int st = decltype(i)::value + 1;
+                issue_stage(std::integral_constant<int, st>{}, st < nk ? st : nk - 1);
+            });
+            wait_vmcnt<(kStages - 2) * kLoadsPerStage>();
         }
         stage_barrier();
         read_b(S0{}, braw);
@@ -344,27 +370,29 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             bqp[0] = widen_pinned(braw[0].x, braw[0].y);
             bqp[1] = widen_pinned(braw[1].x, braw[1].y);
         }
-        // kFull: stages kt + 1 and kt + 2 exist (no bounds checks, so the
-        // steady-state loop body has no branches around the copies)
+        // kFull: stages kt + 1 .. kt + kStages - 1 exist (no bounds checks, so
+        // the steady-state loop body has no branches around the copies)
         auto run_stage = [&](auto cur, auto full, int kt) {
             constexpr int c = decltype(cur)::value;
             constexpr bool kFull = decltype(full)::value;
-            using Next = std::integral_constant<int, (c + 1) % 3>;
-            using Free = std::integral_constant<int, (c + 2) % 3>;  // stage kt + 2's buffer
-            const bool has2 = kFull || kt + 2 < nk;
-            const bool has1 = kFull || kt + 1 < nk;
+            using Next = std::integral_constant<int, (c + 1) % kStages>;
+            // stage kt + kStages - 1's buffer (stage kt - 1's, freed by its barrier)
+            using Free = std::integral_constant<int, (c + kStages - 1) % kStages>;
+            const bool has2 = kStages > 3 || kFull || kt + 2 < nk;
+            const bool has1 = kStages > 3 || kFull || kt + 1 < nk;
+            const int kt_free = kStages > 3 && kt + kStages - 1 >= nk ? nk - 1 : kt + kStages - 1;
             mm_half(0, araw[0], braw, [&](int rm) {
                 if (rm == 0) read_a(cur, 1, araw[1]);
 #pragma unroll
                 for (int i = 0; i < kLoadsPerStage; ++i)
-                    if (rm == (i * RM) / kLoadsPerStage && has2) issue_one(Free{}, kt + 2, i);
+                    if (rm == (i * RM) / kLoadsPerStage && has2) issue_one(Free{}, kt_free, i);
             }, true);
             // mm_half widens braw before the first hook, so the hook may
             // overwrite braw with the next stage's operands
             mm_half(1, araw[1], braw, [&](int rm) {
                 if (rm == kBarrierRm && has1) {
                     // this wave's reads of stage kt have returned, stage kt + 1 has landed
-                    if (has2) wait_vmcnt_lgkm0<kLoadsPerStage>();
+                    if (has2) wait_vmcnt_lgkm0<(kStages - 2) * kLoadsPerStage>();
                     else wait_vmcnt_lgkm0<0>();
                     stage_barrier();
                     read_b(Next{}, braw);
@@ -375,15 +403,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
         using Full = std::true_type;
         using Tail = std::false_type;
         int kt = 0;
-        for (; kt + 5 <= nk; kt += 3) {
-            run_stage(S0{}, Full{}, kt);
-            run_stage(S1{}, Full{}, kt + 1);
-            run_stage(S2{}, Full{}, kt + 2);
-        }
-        for (; kt < nk; kt += 3) {
-            run_stage(S0{}, Tail{}, kt);
-            if (kt + 1 < nk) run_stage(S1{}, Tail{}, kt + 1);
-            if (kt + 2 < nk) run_stage(S2{}, Tail{}, kt + 2);
+        if constexpr (kStages == 3) {
+            for (; kt + 5 <= nk; kt += 3) {
+                run_stage(S0{}, Full{}, kt);
+                run_stage(S1{}, Full{}, kt + 1);
+                run_stage(S2{}, Full{}, kt + 2);
+            }
+            for (; kt < nk; kt += 3) {
+                run_stage(S0{}, Tail{}, kt);
+                if (kt + 1 < nk) run_stage(S1{}, Tail{}, kt + 1);
+                if (kt + 2 < nk) run_stage(S2{}, Tail{}, kt + 2);
+            }
+        } else {
+            for (; kt + kStages <= nk; kt += kStages)
+                static_for<kStages>([&](auto c) { run_stage(c, Full{}, kt + decltype(c)::value); });
+            static_for<kStages>([&](auto c) {
+                if (kt + decltype(c)::value < nk) run_stage(c, Full{}, kt + decltype(c)::value);
+            });
+            wait_vmcnt<0>();  // the repeated copies past the end
         }
     } else {
         // Plain schedule: at the top of stage kt wait for its copies (issued
@@ -647,7 +684,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
     }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int PIPE>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int PIPE, int STAGES = 3>
 bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* partials = nullptr,
                 uint32_t* counters = nullptr) {
     const int tiles_m = (p.M + BM - 1) / BM;
@@ -664,7 +701,7 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
     const dim3 grid(static_cast<uint32_t>(tiles_m * tiles_n * ksplit));
     const dim3 block(64 * WAVES_M * WAVES_N);
 #define FEATHER_LDS_LAUNCH_L(BF, E4, LORA)                                                                            \
-    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, LORA>), grid, block, 0,          \
+    hipLaunchKernelGGL((scaled_mm_lds_kernel<BM, BN, WAVES_M, WAVES_N, PIPE, BF, E4, LORA, STAGES>), grid, block, 0,          \
                        stream, p.a, p.b, p.scale, p.bias, p.c, static_cast<int>(p.M), static_cast<int>(p.N),          \
                        static_cast<int>(p.K), p.has_scale, p.has_bias, tiles_m, tiles_n, group_m, ksplit, partials,   \
                        counters, p.lora_t, p.lora_u, static_cast<int>(p.lora_rank), c_nt)
@@ -708,7 +745,7 @@ bool launch_lds(const MmArgs& p, hipStream_t stream, int ksplit = 1, float* part
 
 template <int PIPE>
 bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks = 1, float* partials = nullptr,
-                     uint32_t* counters = nullptr) {
+                     uint32_t* counters = nullptr, int stages = 3) {
     switch (kernel_id) {
         // 256 x 256 and 256 x 192 on 4 x 2 waves (64 x 128 / 64 x 96 wave tiles:
         // 20% fewer LDS operand bytes per stage than 2 x 4, and wide enough
@@ -719,8 +756,20 @@ bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks 
         case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
         case kLds256x192: return launch_lds<256, 192, 4, 2, PIPE>(p, stream);
         case kLds128x384: return launch_lds<128, 384, 2, 4, PIPE>(p, stream);
-        case kLdsSk64x64: return launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters);
-        case kLdsSk32x128: return launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
+        case kLdsSk64x64:
+        case kLdsSk32x128: {
+            // default schedule: a five- or six-stage ring (see lds_splitk_plan)
+            const bool sk64 = kernel_id == kLdsSk64x64;
+            if constexpr (PIPE == 1) {
+                if (stages == 6)
+                    return sk64 ? launch_lds<64, 64, 1, 4, PIPE, 6>(p, stream, ks, partials, counters)
+                                : launch_lds<32, 128, 1, 4, PIPE, 6>(p, stream, ks, partials, counters);
+                return sk64 ? launch_lds<64, 64, 1, 4, PIPE, 5>(p, stream, ks, partials, counters)
+                            : launch_lds<32, 128, 1, 4, PIPE, 5>(p, stream, ks, partials, counters);
+            }
+            return sk64 ? launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters)
+                        : launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
+        }
         default: return false;
     }
 }
@@ -742,12 +791,22 @@ bool launch_lds_kernel(int kernel_id, const MmArgs& p, hipStream_t stream) {
                                                                  : launch_lds_pipe<1>(kernel_id, p, stream);
 }
 
-// Split-K plan for M <= 64: a 32- or 64-row tile and enough K splits to give
-// about `target` workgroups (each split keeps at least one 64-K stage; no
-// split below 32 stages).
+// Split-K plan for the 32- and 64-row tiles: as many K splits as keep the
+// grid within `target` workgroups (each split keeps at least one 64-K stage;
+// no split below 32 stages), and the stage ring's depth.
 // Measured on MI355X (weights rotated past the MALL): 64 x 64 tiles beat
 // 64 x 128 / 64 x 256 at M = 64 for N = 3072..13824, and 32 x 128 is the best
 // 32-row tile (the small-M kernel still wins at M <= 32).
+// Stage ring and grid (back to back, us, 3 / 5 / 6 stages at the grid this
+// plan picks): M=64 N=13824 K=5120 (216 tiles, one split) 31.1 / 20.9 / 20.8;
+// M=64 N=3072 K=12288 (4 splits) 22.1 / 15.9 / 15.8; M=40 N=13824 K=5120
+// 31.0 / 19.4 / 18.6; M=256 N=3072 K=3072 13.4 / 10.2 / 10.4; M=256
+// N=K=1024 5.60 / 5.18 / 5.37; M=1024 N=K=1024 6.84 / 5.69 / 5.82. The
+// three-stage ring did best with about twice the workgroups (two splits of
+// M=64 N=13824 K=5120: 24.9 us), with which the deeper rings lose (25.5):
+// one workgroup per CU with five or six stages of copies in flight streams
+// better than two sharing a CU with two each, and saves the partial-sum
+// round trip.
 SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     SplitKPlan pl{};
     if (M <= 0 || K % kBK != 0) return pl;
@@ -755,7 +814,7 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     const int bn = bm == 32 ? 128 : 64;
     const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
     const int64_t nk = K / kBK;
-    int64_t ks = (target + tiles - 1) / tiles;
+    int64_t ks = target / tiles;
     // below 32 stages (K < 2048) the split's partial round trip costs more than the stages it
     // spreads (measured: M=256 N=K=1024 6.0 us unsplit vs 7.2 us in 4 splits, M=256 N=2048
     // K=512 4.7 vs 6.7 us; from K=2048 on splitting wins or ties)
@@ -770,6 +829,7 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     pl.ksplit = static_cast<int>(ks);
     pl.tiles = static_cast<int>(tiles);
     pl.counter_bytes = ks > 1 ? kWorkspaceCounterBytes : 0;
+    pl.stages = nk / ks >= 64 ? 6 : 5;
     pl.workspace_bytes = ks > 1 ? pl.counter_bytes + static_cast<size_t>(tiles) * ks * bm * bn * 4 : 0;
     return pl;
 }
@@ -786,8 +846,10 @@ bool launch_lds_splitk(const MmArgs& p, void* workspace, size_t workspace_bytes,
         counters = static_cast<uint32_t*>(workspace);
         partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + pl.counter_bytes);
     }
-    return lds_pipe_env() == 0 && !p.a_bf16 ? launch_lds_pipe<0>(pl.kernel_id, p, stream, ks, partials, counters)
-                                            : launch_lds_pipe<1>(pl.kernel_id, p, stream, ks, partials, counters);
+    const int stages = ks == pl.ksplit ? pl.stages : p.K / kBK >= 64 ? 6 : 5;
+    return lds_pipe_env() == 0 && !p.a_bf16
+               ? launch_lds_pipe<0>(pl.kernel_id, p, stream, ks, partials, counters)
+               : launch_lds_pipe<1>(pl.kernel_id, p, stream, ks, partials, counters, stages);
 }
 
 }  // namespace feather

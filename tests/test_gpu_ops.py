@@ -222,11 +222,17 @@ def test_any_m_equals_padded(cuda, hk, M):
     assert_gemm_close(yp, ref, torch.float16, f"padded {M}")
 
 
-def test_inductor_autotunes_every_compatible_config(cuda, hk, monkeypatch):
+def test_inductor_autotunes_every_compatible_config(cuda, hk, monkeypatch, tmp_path):
     """Inductor's custom-op autotuning (reference kernel/hip/hip_kernel.py:133) on this torch:
     compiling scaled_mm_hip benchmarks the compatible configs through the op's decomposition
-    and the compiled result equals the oracle."""
+    and the compiled result equals the oracle. Inductor's caches are off and its cache
+    directory is fresh: a result cached by an earlier process on the same machine would
+    skip the benchmarking."""
+    import torch._inductor.config as inductor_config
     import torch._inductor.lowering as L
+
+    monkeypatch.setenv("TORCHINDUCTOR_CACHE_DIR", str(tmp_path / "inductor"))
+    monkeypatch.setattr(inductor_config, "force_disable_caches", True)
 
     assert torch.ops.feather_ops_internal.scaled_mm_autotuned.default in L.lowerings
     seen = set()
