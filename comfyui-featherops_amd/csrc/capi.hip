@@ -80,7 +80,8 @@ int tuning_group_m() {
     return g;
 }
 
-// FEATHEROPS_SMALLM_GROUPS: workgroup count the small-M K split aims for (tuning knob, default 256).
+// FEATHEROPS_SMALLM_GROUPS: workgroup count the small-M K split aims for, and the most the
+// split-K LDS tiles' grid may have (tuning knob, default 256).
 int tuning_smallm_groups() {
     static const int g = [] {
         const char* e = getenv("FEATHEROPS_SMALLM_GROUPS");
@@ -90,17 +91,22 @@ int tuning_smallm_groups() {
     return g;
 }
 
-// Split-K LDS tiles (64 x 64, or 32 x 128 for M <= 32) with about 256
+// Split-K LDS tiles (64 x 64, or 32 x 128 for M <= 32) with at most 256
 // workgroups, for K % 64 == 0 and
-//   * 32 < M <= 64: M > 48, or a weight larger than 4096 x 4096 (the small-M
+//   * 16 < M <= 32 and a weight larger than 4096 x 4096 (M=32 N=13824
+//     K=5120: 16.5 us vs 20.3 us for the small-M kernel, M=24 N=K=5120 10.4
+//     vs 11.4 us; at N=K=4096 the small-M kernel wins, 6.5 vs 9.1 us at M=32,
+//     and at M <= 16 it wins or ties: M=16 N=13824 K=5120 15.6 vs 15.2 us,
+//     N=K=8192 15.9 vs 16.6 us);
+//   * 32 < M <= 64: M > 48, or a weight of at least 4096 x 4096 (the small-M
 //     kernel re-reads the activations once per 16-32 columns, which past 32
 //     rows costs more than shared LDS stages plus the split-K reduction;
-//     M=64 N=13824 K=5120: 26 us vs 83 us, while at M=33..48, N=K=4096 the
-//     small-M kernel is 10-15% faster);
-//   * M > 64 when 128 x 128 tiles would not fill the 256 CUs
-//     (ceil(M/128) * ceil(N/128) < 256): M=256 N=K=3072 15 us vs 28 us for the
-//     best tuple tile, M=1024 N=K=1024 8 us vs 11 us; from 256 such tiles on
-//     the tuple's tile wins (M=2048 N=K=3072: 46 us vs 60 us).
+//     M=64 N=13824 K=5120: 20.8 us vs 83 us, M=40 N=K=4096 8.7 vs 9.4 us);
+//   * M > 64 when there would be at most 128 tiles of 128 x 128 (half the
+//     CUs): M=512 N=3072 K=12288 47 us vs 85 us on 128 x 128 tiles, M=1024
+//     N=2048 K=8192 36 vs 54 us, M=2048 N=K=1024 7.4 vs 10.8 us; from 144
+//     such tiles on the tile kernel wins (M=768 N=K=3072 22.5 vs 27.4 us,
+//     M=512 N=K=5120 39.0 vs 44.8 us, M=256 N=13824 K=5120 41.2 vs 49.3 us).
 // Measured on MI355X with the C++ bench. FEATHEROPS_SPLITK (tuning knob, read
 // on every call so that tests can reach the tuple's tile kernels at small
 // shapes): 0 = never, 1 = always (K % 64 == 0).
@@ -109,8 +115,9 @@ int splitk_route(int64_t M, int64_t N, int64_t K) {
     const int v = e ? atoi(e) : -1;
     if (K % 64 != 0 || v == 0) return feather::kKernelNone;
     bool use = v == 1;
-    if (!use && M <= 64) use = M > 48 || (M > 32 && N * K > int64_t(4096) * 4096);
-    if (!use && M > 64) use = ((M + 127) / 128) * ((N + 127) / 128) < 256;
+    if (!use && M <= 64)
+        use = M > 48 || (M > 32 && N * K >= int64_t(4096) * 4096) || (M > 16 && N * K > int64_t(4096) * 4096);
+    if (!use && M > 64) use = ((M + 127) / 128) * ((N + 127) / 128) <= 128;
     return use ? feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).kernel_id : feather::kKernelNone;
 }
 
@@ -119,7 +126,9 @@ int kernel_for(int64_t M, int64_t N, int64_t K, int wm, int wn, int rm, int rn) 
     return sk != feather::kKernelNone ? sk : tile_kernel_for(M, K, wm, wn, rm, rn);
 }
 
-bool is_splitk(int kid) { return kid == feather::kLdsSk64x64 || kid == feather::kLdsSk32x128; }
+bool is_splitk(int kid) {
+    return kid == feather::kLdsSk64x64 || kid == feather::kLdsSk64x128 || kid == feather::kLdsSk32x128;
+}
 
 // Compute units of the current device (256 on an MI355X), read once per device.
 int device_cus() {

@@ -47,6 +47,7 @@ enum KernelId : int {
     kLds128x384 = 26,
     // LDS-DMA tiles with a K split across workgroups (small shapes)
     kLdsSk64x64 = 30,
+    kLdsSk64x128 = 31,
     kLdsSk32x128 = 34,
 };
 

@@ -756,20 +756,17 @@ bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks 
         case kLds128x128: return launch_lds<128, 128, 2, 2, PIPE>(p, stream);
         case kLds256x192: return launch_lds<256, 192, 4, 2, PIPE>(p, stream);
         case kLds128x384: return launch_lds<128, 384, 2, 4, PIPE>(p, stream);
-        case kLdsSk64x64:
-        case kLdsSk32x128: {
-            // default schedule: a five- or six-stage ring (see lds_splitk_plan)
-            const bool sk64 = kernel_id == kLdsSk64x64;
-            if constexpr (PIPE == 1) {
-                if (stages == 6)
-                    return sk64 ? launch_lds<64, 64, 1, 4, PIPE, 6>(p, stream, ks, partials, counters)
-                                : launch_lds<32, 128, 1, 4, PIPE, 6>(p, stream, ks, partials, counters);
-                return sk64 ? launch_lds<64, 64, 1, 4, PIPE, 5>(p, stream, ks, partials, counters)
-                            : launch_lds<32, 128, 1, 4, PIPE, 5>(p, stream, ks, partials, counters);
-            }
-            return sk64 ? launch_lds<64, 64, 1, 4, PIPE>(p, stream, ks, partials, counters)
-                        : launch_lds<32, 128, 1, 4, PIPE>(p, stream, ks, partials, counters);
-        }
+        // default schedule: a five- or six-stage ring (see lds_splitk_plan)
+#define FEATHER_SK(BM_, BN_)                                                                             \
+    if constexpr (PIPE == 1) {                                                                           \
+        if (stages == 6) return launch_lds<BM_, BN_, 1, 4, PIPE, 6>(p, stream, ks, partials, counters); \
+        return launch_lds<BM_, BN_, 1, 4, PIPE, 5>(p, stream, ks, partials, counters);                  \
+    }                                                                                                    \
+    return launch_lds<BM_, BN_, 1, 4, PIPE>(p, stream, ks, partials, counters)
+        case kLdsSk64x64: FEATHER_SK(64, 64);
+        case kLdsSk64x128: FEATHER_SK(64, 128);
+        case kLdsSk32x128: FEATHER_SK(32, 128);
+#undef FEATHER_SK
         default: return false;
     }
 }
@@ -811,21 +808,37 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
     SplitKPlan pl{};
     if (M <= 0 || K % kBK != 0) return pl;
     const int bm = M <= 32 ? 32 : 64;
-    const int bn = bm == 32 ? 128 : 64;
-    const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
     const int64_t nk = K / kBK;
-    int64_t ks = target / tiles;
-    // below 32 stages (K < 2048) the split's partial round trip costs more than the stages it
-    // spreads (measured: M=256 N=K=1024 6.0 us unsplit vs 7.2 us in 4 splits, M=256 N=2048
-    // K=512 4.7 vs 6.7 us; from K=2048 on splitting wins or ties)
-    if (nk < 32) ks = 1;
-    if (ks > nk) ks = nk;
-    if (ks > 32) ks = 32;
-    if (ks < 1) ks = 1;
-    const int64_t per = (nk + ks - 1) / ks;
-    ks = (nk + per - 1) / per;  // no empty split
-    if (tiles > kWorkspaceCounters) ks = 1;  // more tiles than the counter region holds
-    pl.kernel_id = bm == 32 ? kLdsSk32x128 : kLdsSk64x64;
+    auto splits = [&](int64_t tiles) {
+        int64_t ks = target / tiles;
+        // below 32 stages (K < 2048) the split's partial round trip costs more than the stages it
+        // spreads (measured: M=256 N=K=1024 6.0 us unsplit vs 7.2 us in 4 splits, M=256 N=2048
+        // K=512 4.7 vs 6.7 us; from K=2048 on splitting wins or ties)
+        if (nk < 32) ks = 1;
+        if (ks > nk) ks = nk;
+        if (ks > 32) ks = 32;
+        if (ks < 1) ks = 1;
+        const int64_t per = (nk + ks - 1) / ks;
+        ks = (nk + per - 1) / per;  // no empty split
+        if (tiles > kWorkspaceCounters) ks = 1;  // more tiles than the counter region holds
+        return ks;
+    };
+    // 64 rows: 64 x 64 tiles, or 64 x 128 where their grid comes closer to
+    // `target` without passing it (or, past it, is smaller). More splits of
+    // wider tiles lose to the larger partial tiles the last workgroup re-reads
+    // (M=64 N=K=4096, 256 workgroups either way: 8.9 us on 64 x 64, 12.4 us on
+    // 64 x 128), so a tie keeps 64 x 64; M=512 N=3072 K=12288 (384 vs 192
+    // workgroups) 62.0 -> 47.3 us, M=128 N=K=5120 (160 vs 240) 18.6 -> 15.7 us.
+    int bn = bm == 32 ? 128 : 64;
+    if (bm == 64) {
+        const int64_t t64 = (M + 63) / 64 * ((N + 63) / 64), t128 = (M + 63) / 64 * ((N + 127) / 128);
+        const int64_t g64 = t64 * splits(t64), g128 = t128 * splits(t128);
+        const bool wide = g64 > target ? g128 < g64 : g128 <= target && g128 > g64;
+        if (wide) bn = 128;
+    }
+    const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
+    const int64_t ks = splits(tiles);
+    pl.kernel_id = bm == 32 ? kLdsSk32x128 : bn == 128 ? kLdsSk64x128 : kLdsSk64x64;
     pl.ksplit = static_cast<int>(ks);
     pl.tiles = static_cast<int>(tiles);
     pl.counter_bytes = ks > 1 ? kWorkspaceCounterBytes : 0;

@@ -52,11 +52,21 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(32768, 13824, 5120, (4, 2, 4, 4, 8)) == 20  # the same tile and kernel
     assert hk.kernel_id(32768, 13824, 5136, (2, 4, 4, 8, 4)) == 1  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(16, 4096, 4096, (1, 1, 2, 1, 2)) == 10  # small-M
-    assert hk.kernel_id(40, 4096, 4096, (1, 8, 4, 8, 2)) == 10
-    # split-K LDS tiles: 32 < M <= 64 (here M > 48), and shapes 128x128 tiles cannot spread over 256 CUs
+    assert hk.kernel_id(40, 3072, 3072, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(24, 4096, 4096, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(16, 13824, 5120, (1, 8, 4, 8, 2)) == 10
+    # split-K LDS tiles: M > 48; 32 < M <= 48 with a weight of at least 4096 x 4096; 16 < M <= 32
+    # with a larger one (32 x 128 tiles); shapes 128x128 tiles cannot spread over 256 CUs
     assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 30
+    assert hk.kernel_id(40, 4096, 4096, (1, 8, 4, 8, 2)) == 30
+    assert hk.kernel_id(24, 5120, 5120, (1, 8, 4, 8, 2)) == 34
     assert hk.kernel_id(40, 13824, 5120, (1, 1, 2, 1, 2)) == 30
     assert hk.kernel_id(256, 3072, 3072, (2, 4, 4, 8, 4)) == 30
+    # 64 x 128 split-K tiles where 64 x 64 ones would overfill the grid; the tuple's tile from
+    # 144 tiles of 128 x 128 on
+    assert hk.kernel_id(512, 3072, 12288, (2, 2, 4, 4, 4)) == 31
+    assert hk.kernel_id(128, 5120, 5120, (2, 2, 4, 4, 4)) == 31
+    assert hk.kernel_id(768, 3072, 3072, (2, 2, 4, 4, 4)) == 24
     assert hk.kernel_id(2048, 3072, 3072, (2, 2, 4, 4, 4)) == 24
     assert hk.kernel_id(256, 3072, 3088, (2, 2, 4, 4, 4)) == 4  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 23  # BlockM 128, BlockN 256
@@ -306,7 +316,7 @@ def test_splitk_plan_without_counter_room_needs_no_workspace():
 
     code = ("import __graft_entry__; __graft_entry__.load_package();"
             "from featherops_amd.kernel.hip import _lib; L = _lib.lib();"
-            "print(L.feather_scaled_mm_workspace_size(64, 16400 * 64, 2048, 2, 2, 4, 4, 4),"
+            "print(L.feather_scaled_mm_workspace_size(64, 16400 * 128, 2048, 2, 2, 4, 4, 4),"
             " L.feather_scaled_mm_workspace_size(64, 4096, 4096, 2, 2, 4, 4, 4))")
     env = dict(__import__("os").environ, FEATHEROPS_SMALLM_GROUPS="40000")
     out = subprocess.run([sys.executable, "-c", code], cwd=REPO, env=env, capture_output=True, text=True,
