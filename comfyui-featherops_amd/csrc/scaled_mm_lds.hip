@@ -14,8 +14,9 @@
 //     The swizzle is applied on the global side: the lane that fills LDS chunk
 //     p of row r fetches logical chunk p ^ swz(r);
 //   * three LDS stage buffers with two stages of copies in flight behind the
-//     one being multiplied; each barrier is preceded by an explicit vmcnt wait
-//     that leaves the younger stage's copies in flight;
+//     one being multiplied (the split-K tiles: five or six buffers, four or
+//     five stages in flight); each barrier is preceded by an explicit vmcnt
+//     wait that leaves the younger stages' copies in flight;
 //   * per stage, the K halves are processed one after the other (all M
 //     repeats of K half 0, then of K half 1), so only half of the widened B
 //     operands are live at a time;
