@@ -12,6 +12,13 @@
 //   benchmark_hbm_copy --read-bytes B --graph  the same 24 launches captured
 //       once in a HIP graph and replayed (the launch method of a graph-replay
 //       timing of the GEMM)
+//   benchmark_hbm_copy --strip-probe [--n N] [--k K]  the lean small-M
+//       kernel's memory traffic without its arithmetic (M=16, 16-column
+//       strips, one 16-wave workgroup per strip, four 64-K stages in flight
+//       per wave), 24 rotated (K/16, N, 16) weights, back to back: the weight
+//       strip alone, the same bytes read contiguously per workgroup, the strip
+//       plus the activation copies into LDS in the kernel's order, the copies
+//       alone, and three other orders of the same loads
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -19,6 +26,8 @@
 #include <initializer_list>
 #include <iostream>
 #include <string>
+
+#include "../csrc/lds_dma.h"
 
 #define HIP_OK(expr)                                                                                     \
     do {                                                                                                 \
@@ -107,9 +116,148 @@ int read_sweep(const std::initializer_list<int64_t>& sizes, bool graph = false) 
     return 0;
 }
 
+// Probe kinds of --strip-probe. Wave w of workgroup b takes stages w, w + 16,
+// w + 32, w + 48 (64 K each) of 16-column strip b, like the lean small-M kernel.
+enum StripProbe {
+    kStrip = 0,        // weight strip only: per stage one 16-byte load per lane, 4 K groups x 16 columns
+    kContiguous,       // the same byte count, each workgroup reading its own contiguous 64 KB
+    kStripCopies,      // strip + activation copies (rows 0-15 of the stage into LDS), copies issued first
+    kCopies,           // activation copies only
+    kRotated,          // kStripCopies with the stage order rotated per workgroup
+    kWeightsFirst,     // kStripCopies with the weight loads issued before the copies
+    kInterleaved,      // per stage: weight load, then its copies
+    kNumStripProbes
+};
+const char* const kStripProbeName[kNumStripProbes] = {"weight strip only", "contiguous 64 KB per workgroup",
+                                                       "strip + activation copies (kernel order)",
+                                                       "activation copies only", "strip + copies, rotated stages",
+                                                       "strip + copies, weights first",
+                                                       "strip + copies, interleaved per stage"};
+
+template <int KIND>
+__global__ __launch_bounds__(1024) void strip_probe(const uint16_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                    int N, int K, uint32_t* __restrict__ sink) {
+    constexpr int U = 4;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[16 * U * 2048];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int nst = K >> 6;
+    const int n0 = blockIdx.x * 16;
+    const uint32_t slab = feather::lds_addr_of(smem) + wave * (U * 2048);
+    const uint32_t cchunk = static_cast<uint32_t>((lane & 7) * 16);
+    auto stage_of = [&](int st) { return KIND == kRotated ? (st + 4 * static_cast<int>(blockIdx.x)) % nst : st; };
+    auto weight = [&](int st) -> uint4 {
+        if (KIND == kContiguous)
+            return *reinterpret_cast<const uint4*>(B + static_cast<int64_t>(blockIdx.x) * (K / 16) * 256 +
+                                                   static_cast<int64_t>(st) * 1024 + lane * 16);
+        return *reinterpret_cast<const uint4*>(B + (static_cast<int64_t>(st * 4 + lg) * N + n0 + lr) * 16);
+    };
+    auto copies = [&](int st, int u) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            feather::dma16_lds(A, static_cast<uint32_t>(8 * j + (lane >> 3)) * static_cast<uint32_t>(K) * 2u +
+                                      static_cast<uint32_t>(st) * 128u + cchunk,
+                               slab + u * 2048 + j * 1024);
+    };
+    constexpr bool kW = KIND != kCopies;
+    constexpr bool kC = KIND != kStrip && KIND != kContiguous;
+    uint32_t acc = 0;
+    for (int base = wave; base < nst; base += 16 * U) {
+        uint4 v[U];
+        if (KIND == kWeightsFirst) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = weight(base + u * 16);
+        }
+        if (KIND == kInterleaved) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                v[u] = weight(base + u * 16);
+                copies(base + u * 16, u);
+            }
+        } else {
+            if (kC) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (base + u * 16 < nst) copies(stage_of(base + u * 16), u);
+            }
+            if (kW && KIND != kWeightsFirst) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = weight(stage_of(base + u * 16));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        if (kW) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        }
+        if (kC) acc ^= *reinterpret_cast<const uint32_t*>(smem + wave * (U * 2048) + lane * 16);
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live
+}
+
+int strip_probe_run(int N, int K) {
+    if (N % 16 != 0 || K % 4096 != 0) {
+        std::cerr << "--strip-probe: N % 16 == 0 and K % 4096 == 0 (whole rounds of 64 stages)" << std::endl;
+        return 1;
+    }
+    const int nbuf = 24;
+    const int64_t bytes = static_cast<int64_t>(N) * K;
+    uint8_t* bufs[nbuf];
+    for (auto& b : bufs) {
+        HIP_OK(hipMalloc(&b, bytes));
+        HIP_OK(hipMemset(b, 1, bytes));
+    }
+    uint16_t* a;
+    HIP_OK(hipMalloc(&a, static_cast<size_t>(16) * K * 2));
+    HIP_OK(hipMemset(a, 0, static_cast<size_t>(16) * K * 2));
+    uint32_t* sink;
+    HIP_OK(hipMalloc(&sink, 4));
+    hipEvent_t t0, t1;
+    HIP_OK(hipEventCreate(&t0));
+    HIP_OK(hipEventCreate(&t1));
+    auto launch = [&](int kind, const uint8_t* b) {
+        const dim3 grid(N / 16), block(1024);
+        switch (kind) {
+            case kStrip: hipLaunchKernelGGL(strip_probe<kStrip>, grid, block, 0, 0, a, b, N, K, sink); break;
+            case kContiguous: hipLaunchKernelGGL(strip_probe<kContiguous>, grid, block, 0, 0, a, b, N, K, sink); break;
+            case kStripCopies: hipLaunchKernelGGL(strip_probe<kStripCopies>, grid, block, 0, 0, a, b, N, K, sink); break;
+            case kCopies: hipLaunchKernelGGL(strip_probe<kCopies>, grid, block, 0, 0, a, b, N, K, sink); break;
+            case kRotated: hipLaunchKernelGGL(strip_probe<kRotated>, grid, block, 0, 0, a, b, N, K, sink); break;
+            case kWeightsFirst: hipLaunchKernelGGL(strip_probe<kWeightsFirst>, grid, block, 0, 0, a, b, N, K, sink); break;
+            default: hipLaunchKernelGGL(strip_probe<kInterleaved>, grid, block, 0, 0, a, b, N, K, sink); break;
+        }
+    };
+    std::cout << "strip probe M=16 N=" << N << " K=" << K << ", " << nbuf << " rotated weights, back to back" << std::endl;
+    for (int rep = 0; rep < 2; ++rep)
+        for (int kind = 0; kind < kNumStripProbes; ++kind) {
+            for (int i = 0; i < 1000; ++i) launch(kind, bufs[i % nbuf]);
+            HIP_OK(hipEventRecord(t0, 0));
+            for (int i = 0; i < 5000; ++i) launch(kind, bufs[i % nbuf]);
+            HIP_OK(hipEventRecord(t1, 0));
+            HIP_OK(hipEventSynchronize(t1));
+            float ms = 0.f;
+            HIP_OK(hipEventElapsedTime(&ms, t0, t1));
+            std::cout << "  " << kStripProbeName[kind] << ": " << ms * 1000.0 / 5000 << " us/call" << std::endl;
+        }
+    for (auto& b : bufs) HIP_OK(hipFree(b));
+    HIP_OK(hipFree(a));
+    HIP_OK(hipFree(sink));
+    return 0;
+}
+
 int main(int argc, char** argv) {
     int64_t mib = 1024;
     int iters = 20;
+    for (int i = 1; i < argc; ++i)
+        if (std::string(argv[i]) == "--strip-probe") {
+            int n = 4096, k = 4096;
+            for (int j = 1; j + 1 < argc; ++j) {
+                if (std::string(argv[j]) == "--n") n = std::stoi(argv[j + 1]);
+                if (std::string(argv[j]) == "--k") k = std::stoi(argv[j + 1]);
+            }
+            return strip_probe_run(n, k);
+        }
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "--read-sweep") return read_sweep({int64_t(16777216), int64_t(67108864), int64_t(268435456)});
