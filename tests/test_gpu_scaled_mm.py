@@ -656,3 +656,64 @@ def test_large_tiles_every_stage_count(cuda, monkeypatch, K, b_dtype):
             first = y
         else:
             assert torch.equal(y.view(torch.int16), first.view(torch.int16)), f"{cfg} K={K} differs from {LARGE_TILE_CFGS[0]}"
+
+
+# (M, N, K, kernel id, K splits, stage ring depth): every split-K tile width with both ring depths,
+# the ring deeper than a split's stage count (its copies past the end repeat the last stage),
+# ragged M and N
+SPLITK_RING_CASES = [
+    (64, 13824, 5120, 30, 1, 6),
+    (40, 1008, 2048, 30, 16, 5),     # two stages per split, ring of five
+    (1000, 1008, 1024, 30, 1, 5),
+    (512, 3008, 12288, 31, 1, 6),
+    (100, 5120, 5120, 31, 3, 5),
+    (24, 5008, 5120, 34, 6, 5),
+    (32, 13824, 8192, 34, 2, 6),
+    (17, 528, 8192, 34, 32, 5),      # four stages per split
+]
+
+
+@pytest.mark.parametrize("M,N,K,kid,ks,stages", SPLITK_RING_CASES)
+@pytest.mark.parametrize("b_dtype,out_dtype", [(torch.float8_e5m2, torch.float16), (torch.float8_e4m3fn, torch.bfloat16)])
+def test_split_k_tiles_every_width_and_ring(cuda, monkeypatch, M, N, K, kid, ks, stages, b_dtype, out_dtype):
+    """The split-K LDS tiles (64 x 64, 64 x 128, 32 x 128) on five- and six-stage copy rings,
+    through the workspace entry, against a float64 evaluation of the whole output, twice in a
+    row (deterministic, counters back at zero). The kernel id and the split count (read back
+    from the workspace size) are the plan's; the ring depth follows from them (six from 64 K
+    stages per split)."""
+    from gpu_util import stream
+
+    monkeypatch.setenv("FEATHEROPS_SPLITK", "1")
+    cfg = (2, 2, 4, 4, 4)
+    assert lib().feather_scaled_mm_kernel_id(M, N, K, *cfg) == kid
+    bm, bn = {30: (64, 64), 31: (64, 128), 34: (32, 128)}[kid]
+    tiles = (M + bm - 1) // bm * ((N + bn - 1) // bn)
+    nbytes = lib().feather_scaled_mm_workspace_size(M, N, K, *cfg)
+    assert nbytes == (0 if ks == 1 else 65536 + tiles * ks * bm * bn * 4)
+    per = (K // 64 + ks - 1) // ks
+    assert (6 if (K // 64) // ks >= 64 else 5) == stages and per >= 1
+    print("split-K tile", M, N, K, "kernel", kid, "splits", ks, "stages", stages, b_dtype, out_dtype, flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    a = torch.randn(M, K, generator=g).half().to(cuda)
+    fmax = 448.0 if b_dtype == torch.float8_e4m3fn else 57344.0
+    w = torch.randn(N, K, generator=g) * 0.02
+    s = (w.abs().max() / fmax).float().reshape(1)
+    bp = (w / s).to(b_dtype).view(N, K // 16, 16).permute(1, 0, 2).contiguous().to(cuda)
+    del w
+    sd = s.to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.1).to(out_dtype).to(cuda)
+    ref = torch_ref_dev(a, bp, sd, bias, out_dtype, b_dtype=b_dtype)
+    ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=cuda)
+    outs = []
+    for _ in range(2):
+        c = torch.full((M, N), float("nan"), dtype=out_dtype, device=cuda)
+        assert lib().feather_launch_scaled_mm_ws(a.data_ptr(), bp.data_ptr(), sd.data_ptr(), bias.data_ptr(),
+                                                 c.data_ptr(), M, N, K, 1, 1, *cfg,
+                                                 0 if b_dtype == torch.float8_e4m3fn else 1,
+                                                 0 if out_dtype == torch.float16 else 1, ws.data_ptr(), ws.numel(),
+                                                 stream(cuda))
+        torch.cuda.synchronize()
+        assert_gemm_close_dev(c, ref, out_dtype, f"split-K {M}x{N}x{K} kernel {kid}")
+        outs.append(c)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), "split-K reduction must be deterministic"
+    assert (ws[:65536] == 0).all(), "arrival counters must be left at zero"
