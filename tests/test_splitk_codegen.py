@@ -88,7 +88,7 @@ def _check_protocol(name: str, body: list) -> None:
 @pytest.mark.parametrize("src,kernel_re,min_kernels", [
     ("scaled_mm_smallm.hip", r"scaled_mm_smallm_kernel", 8),
     ("lora_down.hip", r"lora_down_kernel", 4),
-    ("scaled_mm_lds.hip", r"scaled_mm_lds_kernelILi(64ELi64|32ELi128)E", 4),
+    ("scaled_mm_lds.hip", r"scaled_mm_lds_kernelILi(64ELi64|64ELi128|32ELi128)E", 12),
 ])
 def test_split_k_arrival_order_in_compiled_code(tmp_path, src, kernel_re, min_kernels):
     bodies = _bodies(_asm(tmp_path, src), kernel_re)
