@@ -8,8 +8,10 @@
 // against 1.6 GFLOP). The kernel is built for that regime:
 //   * a workgroup owns 64 or 128 rows of x and 16 * RN ranks (at most 128)
 //     and walks its K range in 64-wide stages; x rows and D rows (128 bytes
-//     per stage) arrive by whole-cache-line LDS-DMA copies into a three-stage
-//     ring, so the weight-like D is fetched once per row block, not per wave;
+//     per stage) arrive by whole-cache-line LDS-DMA copies into a three- or
+//     four-stage ring that always keeps all but one stage in flight (copies
+//     past a split's end repeat its last stage, so every wait count is a
+//     constant), so the weight-like D is fetched once per row block, not per wave;
 //   * 4 or 8 waves in a (rows/32) x 2 grid: wave (wm, wn) owns 32 rows and
 //     half of the rank tiles, so every operand fragment read from LDS feeds
 //     two MFMAs (16x16x32 fp16/bf16, D as the first operand: lane (lr, lg)
@@ -38,7 +40,7 @@ constexpr int kLdBK = 64;  // K per stage
 
 // WM x WN waves; wave (wm, wn) owns rows 32 wm .. 32 wm + 31 (two 16-row tiles) and
 // rank tiles wn * RN / WN .. of the workgroup's 32 * WM rows x 16 * RN ranks.
-template <int WM, int WN, int RN, bool kBf16>
+template <int WM, int WN, int RN, bool kBf16, int kStagesReq>
 __global__ __launch_bounds__(64 * WM * WN) void lora_down_kernel(const uint16_t* __restrict__ x,
                                                                   const uint16_t* __restrict__ d,
                                                                   uint16_t* __restrict__ t, int M, int K, int R,
@@ -57,7 +59,10 @@ __global__ __launch_bounds__(64 * WM * WN) void lora_down_kernel(const uint16_t*
     constexpr int kXPerWave = kXInst / kWaves;
     constexpr int kDPerWave = (kDInst + kWaves - 1) / kWaves;  // surplus slots repeat the last copy
     constexpr int kLoads = kXPerWave + kDPerWave;
-    __shared__ __attribute__((aligned(1024))) uint8_t sbuf[3][kStage];
+    // stage ring: kStagesReq buffers where they fit in 150 KB of LDS, else as many as fit
+    constexpr int kS = kStagesReq * kStage <= 150 * 1024 ? kStagesReq : 150 * 1024 / kStage;
+    static_assert(kS >= 3, "at least a three-stage ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t sbuf[kS][kStage];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -149,19 +154,24 @@ __global__ __launch_bounds__(64 * WM * WN) void lora_down_kernel(const uint16_t*
         }
     };
 
-    // three-stage ring: copies of stages st + 1 and st + 2 in flight while st is multiplied
-    // (the planner gives every split at least one stage; the guard keeps an
-    // empty split's copies from reading past the ends of x and D regardless)
-    if (nst > 0) issue_stage(0, 0);
-    if (nst > 1) issue_stage(1, 1);
+    // kS-stage ring: copies of stages st + 1 .. st + kS - 2 in flight while st is
+    // multiplied. kS - 1 stages are always in flight: a stage past the split's end
+    // copies its last stage again into a buffer nothing reads, so every wait count
+    // is a constant. (The planner gives every split at least one stage; the guard
+    // keeps an empty split's copies from reading past the ends of x and D regardless.)
+    if (nst > 0) {
+#pragma unroll
+        for (int i = 0; i < kS - 1; ++i) issue_stage(i, i < nst ? i : nst - 1);
+    }
     for (int st = 0; st < nst; ++st) {
-        if (st + 1 < nst) wait_vmcnt<kLoads>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<(kS - 2) * kLoads>();
         stage_barrier();  // stage st landed for every wave; stage st - 1's buffer is free
-        if (st + 2 < nst) issue_stage((st + 2) % 3, st + 2);
-        compute(st % 3, st);
+        const int nx = st + kS - 1;
+        issue_stage(nx % kS, nx < nst ? nx : nst - 1);
+        compute(st % kS, st);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): reads of this buffer done before it is refilled
     }
+    wait_vmcnt<0>();  // the repeated copies past the end
 
     if (ksplit > 1) {
         // partial tile in fragment order ([wave][rn][lane], 16 bytes each) through
@@ -250,13 +260,16 @@ int lora_chunks(int64_t R, LoraChunk out[2]) {
 // else 64 rows (4 waves) with K split across workgroups.
 int lora_rows(int64_t M, int nchunks) { return (M + 127) / 128 * nchunks >= 224 ? 128 : 64; }
 
-// K split for this launch: about one workgroup per CU, at least two stages per split
+// K split for this launch: as many splits as keep the grid within one
+// workgroup per CU (at most 16, at least two stages per split). Rounding the
+// split count down rather than up: M=4608 K=3072 R=64 (72 row blocks, 216 vs
+// 288 workgroups) 2435 vs 2315 GB/s on the four-stage ring.
 int lora_ksplit(int64_t M, int64_t K, int nchunks) {
     const int rows = lora_rows(M, nchunks);
     const int64_t tiles = (M + rows - 1) / rows * nchunks;
     const int64_t nst = (K + kLdBK - 1) / kLdBK;
     if (tiles > kWorkspaceCounters) return 1;
-    int64_t ks = (256 + tiles - 1) / tiles;
+    int64_t ks = 256 / tiles;
     if (ks > nst / 2) ks = nst / 2;
     if (ks > 16) ks = 16;
     if (ks <= 1) return 1;
@@ -282,12 +295,20 @@ void launch_wm(const LoraDownArgs& a, const LoraChunk& c, int ks, float* partial
     constexpr int kRows = 32 * WM;
     const dim3 grid(static_cast<uint32_t>((a.M + kRows - 1) / kRows * ks), static_cast<uint32_t>(c.nchunks));
     const dim3 block(64 * WM * 2);
+    // stage ring: four stages for chunks of up to 64 ranks, three above (GB/s on x + D + T,
+    // back to back, bf16, against the three-stage loop with branches around its tail
+    // copies and a full wait at the tail: M=4096 K=3072 R=32 / 64 / 128 2931 / 2377 / 1834
+    // vs 2763 / 2226 / 1748 (four stages at R=128: 1663); M=4096 K=12288 R=64 3995 vs 3501;
+    // M=4096 K=5120 R=256 1612 vs 1407; M=32768 K=5120 R=64 5440 vs 5412; five and six
+    // stages measured slower on these shapes; at one to four row blocks every form is within
+    // 2% and the earlier loop slightly ahead (M=16 K=3072 R=64: 54.4 vs 55.4 GB/s)
+    constexpr int kS = RN <= 4 ? 4 : 3;
     if (a.bf16)
-        hipLaunchKernelGGL((lora_down_kernel<WM, 2, RN, true>), grid, block, 0, stream, a.x, a.d, a.t,
+        hipLaunchKernelGGL((lora_down_kernel<WM, 2, RN, true, kS>), grid, block, 0, stream, a.x, a.d, a.t,
                            static_cast<int>(a.M), static_cast<int>(a.K), static_cast<int>(a.R), c.r_base, ks, partials,
                            counters);
     else
-        hipLaunchKernelGGL((lora_down_kernel<WM, 2, RN, false>), grid, block, 0, stream, a.x, a.d, a.t,
+        hipLaunchKernelGGL((lora_down_kernel<WM, 2, RN, false, kS>), grid, block, 0, stream, a.x, a.d, a.t,
                            static_cast<int>(a.M), static_cast<int>(a.K), static_cast<int>(a.R), c.r_base, ks, partials,
                            counters);
 }
