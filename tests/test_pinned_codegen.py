@@ -10,8 +10,8 @@ keeps the ordering rules itself. This test checks them in the compiled loops:
   * a widened weight register is written at least one MFMA before the MFMA that reads it (a
     register an MFMA has read as its A or B operand may be overwritten right after it: the
     compiler's own code for builtin MFMAs does that, e.g. in the split-K tiles);
-  * after the main loop, three `s_nop 7` come before the first non-MFMA instruction that reads an
-    accumulator (the epilogue's scaling, the LoRA term)."""
+  * after the last loop, three `s_nop 7` come before any non-MFMA instruction reads an MFMA's
+    result (the epilogue's scaling, the LoRA term)."""
 
 import re
 import subprocess
@@ -141,16 +141,27 @@ def test_widened_weights_written_one_mfma_before_use(bodies):
 
 
 def test_wait_states_before_accumulators_are_read(bodies):
+    """Between the last loop and the pad, no other vector instruction reads a register whose latest
+    write (in program order; the loop's accumulators count as written by MFMAs) was an MFMA. The
+    stages after the last full round of the ring run there, outside any loop, with their own
+    MFMAs; a register the compiler re-initialises with an ordinary move first (the accumulators'
+    zero on the path that skips the loop) is not an MFMA result."""
     for name, body in bodies.items():
         loops = _loops(body)
         end = max(b for _, b in loops)
         pads = [i for i in range(end, len(body) - 2)
                 if all("s_nop 7" in body[i + k] for k in range(3))]
         assert pads, f"{name}: no wait-state pad after the main loop"
-        accs = _loop_accumulators(body)
+        from_mfma = set(_loop_accumulators(body))
         for line in body[end:pads[0]]:
             ins = _instr(line)
-            if not ins or not ins[0].startswith("v_") or ins[0].startswith("v_mfma"):
+            if not ins or not ins[0].startswith("v_"):
                 continue
-            src = set().union(*[_regs(o) for o in ins[1][1:]]) if len(ins[1]) > 1 else set()
-            assert not (src & accs), f"{name}: accumulator read before the wait states: {line.strip()}"
+            op, ops = ins
+            dst = _regs(ops[0]) if ops else set()
+            if op.startswith("v_mfma"):
+                from_mfma |= dst
+                continue
+            src = set().union(*[_regs(o) for o in ops[1:]]) if len(ops) > 1 else set()
+            assert not (src & from_mfma), f"{name}: MFMA result read before the wait states: {line.strip()}"
+            from_mfma -= dst
