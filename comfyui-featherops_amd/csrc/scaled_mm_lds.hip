@@ -762,8 +762,9 @@ bool launch_lds_pipe(int kernel_id, const MmArgs& p, hipStream_t stream, int ks 
     if constexpr (PIPE == 1) {                                                                           \
         if (stages == 6) return launch_lds<BM_, BN_, 1, 4, PIPE, 6>(p, stream, ks, partials, counters); \
         return launch_lds<BM_, BN_, 1, 4, PIPE, 5>(p, stream, ks, partials, counters);                  \
-    }                                                                                                    \
-    return launch_lds<BM_, BN_, 1, 4, PIPE>(p, stream, ks, partials, counters)
+    } else {                                                                                             \
+        return launch_lds<BM_, BN_, 1, 4, PIPE>(p, stream, ks, partials, counters);                     \
+    }
         case kLdsSk64x64: FEATHER_SK(64, 64);
         case kLdsSk64x128: FEATHER_SK(64, 128);
         case kLdsSk32x128: FEATHER_SK(32, 128);
