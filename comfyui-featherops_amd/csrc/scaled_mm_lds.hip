@@ -371,8 +371,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void scaled_mm_lds_kernel(
             bqp[0] = widen_pinned(braw[0].x, braw[0].y);
             bqp[1] = widen_pinned(braw[1].x, braw[1].y);
         }
-        // kFull: stages kt + 1 .. kt + kStages - 1 exist (no bounds checks, so
-        // the steady-state loop body has no branches around the copies)
+        // kFull (three-stage ring): stages kt + 1 and kt + 2 exist (no bounds
+        // checks, so the steady-state loop body has no branches around the
+        // copies; a checked copy of the loop runs the last three to five
+        // stages). Deeper rings run every stage unchecked, the copies of
+        // stages past the end clamped to the last one.
         auto run_stage = [&](auto cur, auto full, int kt) {
             constexpr int c = decltype(cur)::value;
             constexpr bool kFull = decltype(full)::value;
