@@ -102,11 +102,13 @@ int tuning_smallm_groups() {
 //     kernel re-reads the activations once per 16-32 columns, which past 32
 //     rows costs more than shared LDS stages plus the split-K reduction;
 //     M=64 N=13824 K=5120: 20.8 us vs 83 us, M=40 N=K=4096 8.7 vs 9.4 us);
-//   * M > 64 when there would be at most 128 tiles of 128 x 128 (half the
-//     CUs): M=512 N=3072 K=12288 47 us vs 85 us on 128 x 128 tiles, M=1024
-//     N=2048 K=8192 36 vs 54 us, M=2048 N=K=1024 7.4 vs 10.8 us; from 144
-//     such tiles on the tile kernel wins (M=768 N=K=3072 22.5 vs 27.4 us,
-//     M=512 N=K=5120 39.0 vs 44.8 us, M=256 N=13824 K=5120 41.2 vs 49.3 us).
+//   * M > 64 when the split-K plan's grid fits one round of `target`
+//     workgroups (each holds a CU's LDS, so a larger grid runs twice):
+//     M=154 N=10240 K=4096 19.9 us vs 32.0 us on 128 x 128 tiles, M=512
+//     N=3072 K=12288 47 vs 85 us, M=1024 N=2048 K=8192 36 vs 54 us, M=2048
+//     N=K=1024 7.4 vs 10.8 us; past it the tile kernel wins (M=256 N=10240
+//     K=4096: 320 workgroups, 38.2 vs 32.7 us; M=768 N=K=3072 27.4 vs 22.5 us,
+//     M=512 N=K=5120 44.8 vs 39.0 us, M=256 N=13824 K=5120 49.3 vs 41.2 us).
 // Measured on MI355X with the C++ bench. FEATHEROPS_SPLITK (tuning knob, read
 // on every call so that tests can reach the tuple's tile kernels at small
 // shapes): 0 = never, 1 = always (K % 64 == 0).
@@ -117,8 +119,9 @@ int splitk_route(int64_t M, int64_t N, int64_t K) {
     bool use = v == 1;
     if (!use && M <= 64)
         use = M > 48 || (M > 32 && N * K >= int64_t(4096) * 4096) || (M > 16 && N * K > int64_t(4096) * 4096);
-    if (!use && M > 64) use = ((M + 127) / 128) * ((N + 127) / 128) <= 128;
-    return use ? feather::lds_splitk_plan(M, N, K, tuning_smallm_groups()).kernel_id : feather::kKernelNone;
+    const feather::SplitKPlan pl = feather::lds_splitk_plan(M, N, K, tuning_smallm_groups());
+    if (!use && M > 64) use = static_cast<int64_t>(pl.tiles) * pl.ksplit <= tuning_smallm_groups();
+    return use ? pl.kernel_id : feather::kKernelNone;
 }
 
 int kernel_for(int64_t M, int64_t N, int64_t K, int wm, int wn, int rm, int rn) {

@@ -62,11 +62,13 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(24, 5120, 5120, (1, 8, 4, 8, 2)) == 34
     assert hk.kernel_id(40, 13824, 5120, (1, 1, 2, 1, 2)) == 30
     assert hk.kernel_id(256, 3072, 3072, (2, 4, 4, 8, 4)) == 30
-    # 64 x 128 split-K tiles where 64 x 64 ones would overfill the grid; the tuple's tile from
-    # 144 tiles of 128 x 128 on
+    # 64 x 128 split-K tiles where 64 x 64 ones would overfill the grid
     assert hk.kernel_id(512, 3072, 12288, (2, 2, 4, 4, 4)) == 31
     assert hk.kernel_id(128, 5120, 5120, (2, 2, 4, 4, 4)) == 31
     assert hk.kernel_id(768, 3072, 3072, (2, 2, 4, 4, 4)) == 24
+    # M > 64 takes the split-K tiles when their grid fits one round of 256 workgroups
+    assert hk.kernel_id(154, 10240, 4096, (2, 2, 4, 4, 4)) == 31  # 240 workgroups of 64 x 128
+    assert hk.kernel_id(256, 10240, 4096, (2, 2, 4, 4, 4)) == 24  # 320: the 128 x 128 tuple tile
     assert hk.kernel_id(2048, 3072, 3072, (2, 2, 4, 4, 4)) == 24
     assert hk.kernel_id(256, 3072, 3088, (2, 2, 4, 4, 4)) == 4  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(4096, 4096, 4096, (1, 8, 4, 8, 2)) == 23  # BlockM 128, BlockN 256
