@@ -98,10 +98,13 @@ int tuning_smallm_groups() {
 //     vs 11.4 us; at N=K=4096 the small-M kernel wins, 6.5 vs 9.1 us at M=32,
 //     and at M <= 16 it wins or ties: M=16 N=13824 K=5120 15.6 vs 15.2 us,
 //     N=K=8192 15.9 vs 16.6 us);
-//   * 32 < M <= 64: M > 48, or a weight of at least 4096 x 4096 (the small-M
-//     kernel re-reads the activations once per 16-32 columns, which past 32
-//     rows costs more than shared LDS stages plus the split-K reduction;
-//     M=64 N=13824 K=5120: 20.8 us vs 83 us, M=40 N=K=4096 8.7 vs 9.4 us);
+//   * 32 < M <= 64: M > 48, N >= 3072, or a weight of at least 4096 x 4096
+//     (the small-M kernel re-reads the activations once per 16-32 columns,
+//     which past 32 rows costs more than shared LDS stages plus the split-K
+//     reduction: M=64 N=13824 K=5120 20.8 us vs 83 us, M=33 N=K=3072 7.7 vs
+//     11.3 us, M=40 N=8192 K=1024 5.4 vs 9.4 us, M=48 N=5120 K=3072 8.2 vs
+//     15.0 us; narrower weights need 8-16 K splits and stay on the small-M
+//     kernel: M=33 N=K=2048 7.1 vs 7.8 us, M=40 N=1024 K=8192 10.9 vs 11.8 us);
 //   * M > 64 when the split-K plan's grid fits one round of `target`
 //     workgroups (each holds a CU's LDS, so a larger grid runs twice):
 //     M=154 N=10240 K=4096 19.9 us vs 32.0 us on 128 x 128 tiles, M=512
@@ -118,7 +121,8 @@ int splitk_route(int64_t M, int64_t N, int64_t K) {
     if (K % 64 != 0 || v == 0) return feather::kKernelNone;
     bool use = v == 1;
     if (!use && M <= 64)
-        use = M > 48 || (M > 32 && N * K >= int64_t(4096) * 4096) || (M > 16 && N * K > int64_t(4096) * 4096);
+        use = M > 48 || (M > 32 && (N >= 3072 || N * K >= int64_t(4096) * 4096)) ||
+              (M > 16 && N * K > int64_t(4096) * 4096);
     const feather::SplitKPlan pl = feather::lds_splitk_plan(M, N, K, tuning_smallm_groups());
     if (!use && M > 64) use = static_cast<int64_t>(pl.tiles) * pl.ksplit <= tuning_smallm_groups();
     return use ? pl.kernel_id : feather::kKernelNone;

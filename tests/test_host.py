@@ -52,13 +52,15 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(32768, 13824, 5120, (4, 2, 4, 4, 8)) == 20  # the same tile and kernel
     assert hk.kernel_id(32768, 13824, 5136, (2, 4, 4, 8, 4)) == 1  # K % 64 != 0: register-staged tile
     assert hk.kernel_id(16, 4096, 4096, (1, 1, 2, 1, 2)) == 10  # small-M
-    assert hk.kernel_id(40, 3072, 3072, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(40, 2048, 2048, (1, 8, 4, 8, 2)) == 10
+    assert hk.kernel_id(40, 1024, 8192, (1, 8, 4, 8, 2)) == 10
     assert hk.kernel_id(24, 4096, 4096, (1, 8, 4, 8, 2)) == 10
     assert hk.kernel_id(16, 13824, 5120, (1, 8, 4, 8, 2)) == 10
-    # split-K LDS tiles: M > 48; 32 < M <= 48 with a weight of at least 4096 x 4096; 16 < M <= 32
-    # with a larger one (32 x 128 tiles); shapes 128x128 tiles cannot spread over 256 CUs
+    # split-K LDS tiles: M > 48; 32 < M <= 48 with N >= 3072 or a weight of at least 4096 x 4096;
+    # 16 < M <= 32 with a larger one (32 x 128 tiles); larger M when the grid fits one round
     assert hk.kernel_id(64, 4096, 4096, (1, 8, 4, 8, 2)) == 30
     assert hk.kernel_id(40, 4096, 4096, (1, 8, 4, 8, 2)) == 30
+    assert hk.kernel_id(33, 3072, 3072, (1, 8, 4, 8, 2)) == 30
     assert hk.kernel_id(24, 5120, 5120, (1, 8, 4, 8, 2)) == 34
     assert hk.kernel_id(40, 13824, 5120, (1, 1, 2, 1, 2)) == 30
     assert hk.kernel_id(256, 3072, 3072, (2, 4, 4, 8, 4)) == 30
