@@ -206,3 +206,34 @@ def test_random_large_shapes_e4m3_bf16_activations(cuda, hk):
         y = hk.scaled_mm_hip_any_m(a, bp, s, bias, out)
         assert_gemm_close_dev(y, ref, out, f"large e4m3/bf16 {case}")
         del ref, y
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_split_k_region(cuda, hk, seed):
+    """Random shapes around the split-K routes (17 <= M <= 2048, N and K 1024..10240) through the
+    any-M entry with its default routing: the small-M kernel, the split-K tiles (64 x 64, 64 x 128,
+    32 x 128 on five- or six-stage rings, K splits from one to many) or the tile kernels, whichever
+    the shape takes; the whole output against a float64 evaluation on the device, and the kernel
+    each case took is printed."""
+    from gpu_util import assert_gemm_close_dev, torch_ref_dev
+
+    rng = np.random.default_rng(100 + seed)
+    for case in range(16):
+        M = int(rng.choice([17, 24, 33, 40, 48, 56, 64, 77, 154, 256, 512, 1024, 2048]))
+        N = 16 * int(rng.integers(64, 641))
+        K = 64 * int(rng.integers(16, 161))
+        out = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        b_dtype = torch.float8_e4m3fn if rng.random() < 0.3 else torch.float8_e5m2
+        kid = hk.kernel_id(M, N, K, hk.any_m_config(M, N, K))
+        print(f"seed {seed} case {case}: M={M} N={N} K={K} {out} {b_dtype} kernel {kid}", flush=True)
+        g = torch.Generator(device=cuda).manual_seed(1000 * seed + case)
+        a = torch.randn(M, K, generator=g, device=cuda).half()
+        fmax = 448.0 if b_dtype == torch.float8_e4m3fn else 57344.0
+        w = torch.randn(N, K, generator=g, device=cuda) * 0.02
+        s = (w.abs().max() / fmax).float().reshape(())
+        bp = (w / s).to(b_dtype).view(N, K // 16, 16).permute(1, 0, 2).contiguous()
+        del w
+        bias = (torch.randn(N, generator=g, device=cuda) * 0.1).to(out)
+        y = hk.scaled_mm_hip_any_m(a, bp, s, bias, out)
+        ref = torch_ref_dev(a, bp, s, bias, out, b_dtype=b_dtype)
+        assert_gemm_close_dev(y, ref, out, f"seed {seed} case {case}: M={M} N={N} K={K} kernel {kid}")
