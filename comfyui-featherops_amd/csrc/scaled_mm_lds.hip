@@ -829,16 +829,22 @@ SplitKPlan lds_splitk_plan(int64_t M, int64_t N, int64_t K, int target) {
         return ks;
     };
     // 64 rows: 64 x 64 tiles, or 64 x 128 where their grid comes closer to
-    // `target` without passing it (or, past it, is smaller). More splits of
-    // wider tiles lose to the larger partial tiles the last workgroup re-reads
-    // (M=64 N=K=4096, 256 workgroups either way: 8.9 us on 64 x 64, 12.4 us on
-    // 64 x 128), so a tie keeps 64 x 64; M=512 N=3072 K=12288 (384 vs 192
-    // workgroups) 62.0 -> 47.3 us, M=128 N=K=5120 (160 vs 240) 18.6 -> 15.7 us.
+    // `target` without passing it (or, past it, is smaller) in at most four K
+    // splits. The last workgroup of a tile re-reads every split's partial
+    // tile (32 KB at 64 x 128), so many splits of wide tiles lose: M=64 N=K=4096
+    // (256 workgroups either way) 8.9 us on 64 x 64, 12.4 us on 64 x 128;
+    // M=64 N=2176 K=8128 (238 workgroups in 7 splits vs 255 in 15) 10.6 vs
+    // 17.1 us; M=64 N=6144 K=4096 (192 in 2 vs 240 in 5) 11.7 vs 12.7 us. Where
+    // the wide grid is larger in few splits it wins: M=512 N=3072 K=12288 (384
+    // vs 192 workgroups) 62.0 -> 47.3 us, M=128 N=K=5120 (160 vs 240 in 3
+    // splits) 18.6 -> 15.7 us, M=48 N=9728 K=7488 (152 vs 228) 24.7 -> 20.5 us,
+    // M=77 N=6448 K=10048 (202 vs 204 in 2) 28.4 -> 25.4 us (M=40 N=5552
+    // K=6976, 174 vs 220 in 5 splits, would gain 5%).
     int bn = bm == 32 ? 128 : 64;
     if (bm == 64) {
         const int64_t t64 = (M + 63) / 64 * ((N + 63) / 64), t128 = (M + 63) / 64 * ((N + 127) / 128);
         const int64_t g64 = t64 * splits(t64), g128 = t128 * splits(t128);
-        const bool wide = g64 > target ? g128 < g64 : g128 <= target && g128 > g64;
+        const bool wide = (g64 > target ? g128 < g64 : g128 <= target && g128 > g64) && splits(t128) <= 4;
         if (wide) bn = 128;
     }
     const int64_t tiles = (M + bm - 1) / bm * ((N + bn - 1) / bn);
