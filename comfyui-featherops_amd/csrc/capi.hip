@@ -93,11 +93,14 @@ int tuning_smallm_groups() {
 
 // Split-K LDS tiles (64 x 64, or 32 x 128 for M <= 32) with at most 256
 // workgroups, for K % 64 == 0 and
-//   * 16 < M <= 32 and a weight larger than 4096 x 4096 (M=32 N=13824
-//     K=5120: 16.5 us vs 20.3 us for the small-M kernel, M=24 N=K=5120 10.4
-//     vs 11.4 us; at N=K=4096 the small-M kernel wins, 6.5 vs 9.1 us at M=32,
-//     and at M <= 16 it wins or ties: M=16 N=13824 K=5120 15.6 vs 15.2 us,
-//     N=K=8192 15.9 vs 16.6 us);
+//   * 16 < M <= 32 and a weight larger than 4096 x 4096, unless the small-M
+//     plan runs unsplit in one round of 16-column strips (N <= 4096): M=32
+//     N=13824 K=5120 16.5 us vs 20.3 us for the small-M kernel, M=24 N=K=5120
+//     10.4 vs 11.4 us, M=32 N=3072 K=12288 13.7 vs 16.6 us, but M=24 N=3280
+//     K=6016 (unsplit, 205 strips) 6.9 us on the small-M kernel vs 10.2; at
+//     N=K=4096 the small-M kernel wins, 6.5 vs 9.1 us at M=32, and at M <= 16
+//     it wins or ties: M=16 N=13824 K=5120 15.6 vs 15.2 us, N=K=8192 15.9 vs
+//     16.6 us);
 //   * 32 < M <= 64: M > 48, N >= 3072, or a weight of at least 4096 x 4096
 //     (the small-M kernel re-reads the activations once per 16-32 columns,
 //     which past 32 rows costs more than shared LDS stages plus the split-K
@@ -122,7 +125,8 @@ int splitk_route(int64_t M, int64_t N, int64_t K) {
     bool use = v == 1;
     if (!use && M <= 64)
         use = M > 48 || (M > 32 && (N >= 3072 || N * K >= int64_t(4096) * 4096)) ||
-              (M > 16 && N * K > int64_t(4096) * 4096);
+              (M > 16 && N * K > int64_t(4096) * 4096 &&
+               (N > 4096 || feather::smallm_ksplit(M, N, K, tuning_smallm_groups()) > 1));
     const feather::SplitKPlan pl = feather::lds_splitk_plan(M, N, K, tuning_smallm_groups());
     if (!use && M > 64) use = static_cast<int64_t>(pl.tiles) * pl.ksplit <= tuning_smallm_groups();
     return use ? pl.kernel_id : feather::kKernelNone;

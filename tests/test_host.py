@@ -62,6 +62,8 @@ def test_kernel_id_mapping(hk):
     assert hk.kernel_id(40, 4096, 4096, (1, 8, 4, 8, 2)) == 30
     assert hk.kernel_id(33, 3072, 3072, (1, 8, 4, 8, 2)) == 30
     assert hk.kernel_id(24, 5120, 5120, (1, 8, 4, 8, 2)) == 34
+    assert hk.kernel_id(24, 2800, 9984, (1, 8, 4, 8, 2)) == 34  # the small-M plan would split K
+    assert hk.kernel_id(24, 3280, 6016, (1, 8, 4, 8, 2)) == 10  # unsplit, one round of strips
     assert hk.kernel_id(40, 13824, 5120, (1, 1, 2, 1, 2)) == 30
     assert hk.kernel_id(256, 3072, 3072, (2, 4, 4, 8, 4)) == 30
     # 64 x 128 split-K tiles where 64 x 64 ones would overfill the grid
